@@ -1,0 +1,115 @@
+// MI355X (gfx950) routed-expert kernels for the IQ_K relayout: the C ABI.
+//
+// This library replaces the reference's kernel seam: Metal source built per
+// geometry and dispatched through mx.fast.metal_kernel (reference:
+// src/mlx_iqk/kernels.py:751-887, called from src/mlx_iqk/nn.py:155-271).
+// Every entry point is asynchronous on the caller's HIP stream (`stream` is
+// a hipStream_t; NULL is the default stream), takes device pointers only,
+// allocates nothing and never synchronises.
+//
+// Return codes: IQK_OK, or a refusal raised before anything is launched
+// (unknown member, unsized geometry, bad argument), or IQK_ERR_LAUNCH with the
+// HIP error kept for iqk_hip_last_error().  The reference refuses the same
+// geometries in Python before compiling (src/mlx_iqk/kernels.py:100-142);
+// here the refusal is also enforced at the ABI, so a caller that skips the
+// Python guards still cannot launch an unsized kernel.
+//
+// Streams: the member's relayout streams in component order, each a
+// contiguous stacked tensor [num_experts, out_features, ...]:
+//   IQ2_KS   qs u32, scl u8, sch u8, sex u8, dv f16        (5 streams)
+//   IQ2_K    qs u32, scl u8, sex u8, dv f16                (4 streams)
+//   IQ1_S_R4 qs u32, qh u16, dv f16                        (3 streams)
+// The shared tables (the fp16 alphabet, the IQ1_S grid) are compiled into
+// the library; the reference passes them as kernel inputs instead
+// (src/mlx_iqk/nn.py:56-94).
+//
+// Expert ids read from device memory are bounds-checked in the kernels: an
+// id >= num_experts produces NaN outputs for that pair (or skips that expert
+// in the producer), never an out-of-bounds read.
+#ifndef IQK_HIP_H
+#define IQK_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IQK_HIP_ABI_VERSION 1
+
+#define IQK_MEMBER_IQ2_KS 0
+#define IQK_MEMBER_IQ2_K 1
+#define IQK_MEMBER_IQ1_S_R4 2
+
+#define IQK_OK 0
+#define IQK_ERR_MEMBER 1
+#define IQK_ERR_GEOMETRY 2
+#define IQK_ERR_ARGUMENT 3
+#define IQK_ERR_LAUNCH 4
+
+int iqk_hip_abi_version(void);
+// The hipError_t of the most recent IQK_ERR_LAUNCH on this thread (0 if none).
+int iqk_hip_last_error(void);
+// Geometry guards, the ABI form of check_gemv_geometry / check_dequant_geometry
+// (reference: src/mlx_iqk/kernels.py:100-129): IQK_OK or the refusal code.
+int iqk_check_gemv_geometry(int member, int64_t in_features, int64_t out_features);
+int iqk_check_dequant_geometry(int member, int64_t in_features, int64_t out_features);
+
+// Decode GEMV over token-expert pairs (replaces gemv_kernel + its dispatch,
+// src/mlx_iqk/kernels.py:792-810, src/mlx_iqk/nn.py:240-271):
+//   y[m, r] = fp16( sum_k W[sel[m]][r][k] * x[m / pairs_per_row][k] )
+// x: f16 [mats / pairs_per_row, in_features]; sel: u32 [mats] (device);
+// y: f16 [mats, out_features].  pairs_per_row is the reference's `dims`.
+int iqk_gemv(int member, int64_t in_features, int64_t out_features, int64_t num_experts,
+             const void *x, const void *const *streams, int n_streams,
+             const uint32_t *sel, uint32_t pairs_per_row, uint32_t mats,
+             void *y, void *stream);
+
+// The GEMV's deleted-decode floor: identical loads, the decode replaced by an
+// integer fold of every loaded word that reaches y (reference:
+// bench/floors.py:86-176).  Same arguments; y holds no meaningful values.
+int iqk_gemv_floor(int member, int64_t in_features, int64_t out_features, int64_t num_experts,
+                   const void *x, const void *const *streams, int n_streams,
+                   const uint32_t *sel, uint32_t pairs_per_row, uint32_t mats,
+                   void *y, void *stream);
+
+// Stacked-expert dequant producer (replaces dequant_kernel + dispatch,
+// src/mlx_iqk/kernels.py:855-869, src/mlx_iqk/nn.py:155-169):
+//   w[slot(e)][r][k] = fp16( d * float(index) * value )   bit-exact,
+// for every source expert e < num_experts with 0 <= slot(e) < n_slots;
+// slot(e) = slot_of_expert[e] (device i32 [num_experts]) or e when the
+// pointer is NULL.  Experts with no slot are skipped.  w: f16 [n_slots,
+// out_features, in_features].
+int iqk_dequant(int member, int64_t in_features, int64_t out_features, int64_t num_experts,
+                const void *const *streams, int n_streams,
+                const int32_t *slot_of_expert, int64_t n_slots,
+                void *w, void *stream);
+
+// The producer's floor: identical loads and stores, decode deleted
+// (reference: bench/floors.py:179-220).
+int iqk_dequant_floor(int member, int64_t in_features, int64_t out_features, int64_t num_experts,
+                      const void *const *streams, int n_streams,
+                      const int32_t *slot_of_expert, int64_t n_slots,
+                      void *w, void *stream);
+
+// Sorted grouped GEMM on fp16 MFMA with f32 accumulation, the prefill
+// contraction (replaces mx.gather_mm(x, W.swapaxes(-1,-2), rhs_indices,
+// sorted_indices=True), src/mlx_iqk/nn.py:221-238).  Work items ("slots")
+// are sorted by group; group g owns slots [group_offsets[g],
+// group_offsets[g+1]).  For slot p:
+//   y[y_rows[p]][n] = fp16( sum_k x[x_rows[p]][k] * w[g][n][k] )
+// x: f16 [n_x_rows, in_features]; w: f16 [n_groups, out_features, in_features];
+// y: f16 [n_slots, out_features]; group_offsets: u32 [n_groups + 1] (device,
+// non-decreasing, last = n_slots); x_rows, y_rows: u32 [n_slots] (device;
+// y_rows NULL = identity, else a permutation of [0, n_slots)).  Device-side
+// indices out of range are skipped, never dereferenced.
+int iqk_grouped_gemm(int64_t in_features, int64_t out_features, int64_t n_groups, int64_t n_slots,
+                     const void *x, int64_t n_x_rows, const void *w, const uint32_t *group_offsets,
+                     const uint32_t *x_rows, const uint32_t *y_rows, void *y, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif  // IQK_HIP_H

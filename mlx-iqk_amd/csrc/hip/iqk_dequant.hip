@@ -1,0 +1,222 @@
+// Stacked-expert dequant producer and its floor (gfx950).
+//
+// Reference: the Metal dequantization (src/mlx_iqk/kernels.py:580-676,
+// launched by src/mlx_iqk/nn.py:155-169) and its floor
+// (bench/floors.py:179-220).
+//
+// One thread reconstructs 64 consecutive weights of one row and writes them
+// with eight 128-bit stores; a 64-lane wavefront writes 4 KiB of
+// contiguous fp16.  Bit-exactness: every weight is the CPU dequantizer's f32
+// chain dl = d * float(index), y = dl * float(value), each product exact, then
+// one round-to-nearest-even conversion.  Because a sub-block has only four
+// distinct values, the four fp16 results are formed once per sub-block and
+// each pair of output weights is one v_perm_b32 from that 8-byte table; the
+// table entry for a code is exactly the value the per-weight chain would
+// produce.
+//
+// The producer writes the experts the caller selects into compact slots
+// (slot_of_expert), so a prefill reconstructs each routed expert once.
+
+#include "iqk_device.h"
+#include "iqk_host.h"
+
+#define IQK_GRID_STORAGE __constant__ static const
+#include "../iq1s_grid.h"
+
+namespace iqk {
+
+struct DequantArgs {
+    const void *s0, *s1, *s2, *s3, *s4;
+    const int32_t *slot_of_expert;
+    uint32_t num_experts;
+    uint32_t out_features;
+    uint32_t n_slots;
+    uint16_t *w;
+};
+
+// Four fp16 values as a v_perm pool: low bytes in slots 0-3, high bytes in
+// slots 4-7, so the selector for a code c is (c, 4+c).
+struct Pool {
+    uint32_t lo, hi;
+};
+
+__device__ __forceinline__ Pool make_pool(float v0, float v1, float v2, float v3) {
+    const uint32_t p01 = float_to_half_bits(v0) | (float_to_half_bits(v1) << 16);
+    const uint32_t p23 = float_to_half_bits(v2) | (float_to_half_bits(v3) << 16);
+    return {perm(p23, p01, 0x06040200u), perm(p23, p01, 0x07050301u)};
+}
+
+// 16 codes of one word -> 8 dwords of fp16 pairs in k order.  Weight k's
+// code sits in byte k/4 of e[k%4]; output dword 2b pairs weights (4b, 4b+1),
+// dword 2b+1 pairs (4b+2, 4b+3).  A first perm spreads the two codes to
+// (ca, ca, cb, cb), the or makes it the lookup selector (ca, 4+ca, cb, 4+cb).
+__device__ __forceinline__ void expand_word(uint32_t qw, Pool p, uint32_t *out) {
+    const uint32_t e0 = qw & 0x03030303u;
+    const uint32_t e1 = (qw >> 2) & 0x03030303u;
+    const uint32_t e2 = (qw >> 4) & 0x03030303u;
+    const uint32_t e3 = (qw >> 6) & 0x03030303u;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const uint32_t spread = uint32_t(b) * 0x00000101u + uint32_t(b + 4) * 0x01010000u;
+        const uint32_t s01 = perm(e1, e0, spread) | 0x04000400u;
+        const uint32_t s23 = perm(e3, e2, spread) | 0x04000400u;
+        out[2 * b] = perm(p.hi, p.lo, s01);
+        out[2 * b + 1] = perm(p.hi, p.lo, s23);
+    }
+}
+
+template <int MEMBER, int N, bool FLOOR>
+__global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
+    constexpr int TPR = N / 64;  // threads per row
+    __shared__ uint16_t grid[MEMBER == IQ1_S_R4 ? IQK_IQ1S_GRID_SIZE : 1];
+    if constexpr (MEMBER == IQ1_S_R4 && !FLOOR) {
+        for (int i = threadIdx.x; i < IQK_IQ1S_GRID_SIZE; i += blockDim.x) grid[i] = iqk_iq1s_grid_codes[i];
+        __syncthreads();
+    }
+    const uint64_t gid = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const uint64_t row = gid / TPR;  // stacked source row
+    const int lc = int(gid % TPR);
+    const uint32_t expert = uint32_t(row / a.out_features);
+    if (expert >= a.num_experts) return;
+    const int32_t slot = a.slot_of_expert ? a.slot_of_expert[expert] : int32_t(expert);
+    if (slot < 0 || uint32_t(slot) >= a.n_slots) return;
+    const uint32_t r = uint32_t(row - uint64_t(expert) * a.out_features);
+    uint16_t *dst = a.w + (uint64_t(slot) * a.out_features + r) * N + 64 * lc;
+
+    uint32_t out[32];
+    if constexpr (MEMBER == IQ2_KS || MEMBER == IQ2_K) {
+        const uint4_t q = load_u4(static_cast<const uint32_t *>(a.s0) + row * (N / 16) + 4 * lc);
+        uint32_t sc, hb = 0, ab, dvb;
+        if constexpr (MEMBER == IQ2_KS) {
+            sc = static_cast<const uint8_t *>(a.s1)[row * (N / 64) + lc];
+            hb = static_cast<const uint8_t *>(a.s2)[row * (N / 256) + lc / 4];
+            ab = static_cast<const uint8_t *>(a.s3)[row * (N / 256) + lc / 4];
+            dvb = static_cast<const uint16_t *>(a.s4)[row];
+        } else {
+            sc = static_cast<const uint16_t *>(a.s1)[row * (N / 64) + lc];
+            ab = static_cast<const uint8_t *>(a.s2)[row * (N / 128) + lc / 2];
+            dvb = static_cast<const uint16_t *>(a.s3)[row * (N / 256) + lc / 4];
+        }
+        if constexpr (FLOOR) {
+            const uint32_t iacc = q.x + 3u * q.y + 5u * q.z + 7u * q.w + 59u * sc + 61u * hb + 71u * ab + 67u * dvb;
+            const uint32_t hv = float_to_half_bits(float(iacc & 0xffu));
+#pragma unroll
+            for (int i = 0; i < 32; ++i) out[i] = hv | (hv << 16);
+        } else {
+            const float d = half_bits_to_float(dvb);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                uint32_t idx, alpha;
+                if constexpr (MEMBER == IQ2_KS) {  // sub-block 2*lc + w/2 (32 weights)
+                    const int t = w / 2, bsh = 2 * (lc % 4);
+                    idx = ((sc >> (4 * t)) & 15u) | (((hb >> (bsh + t)) & 1u) << 4);
+                    idx -= 16u;
+                    alpha = (ab >> (bsh + t)) & 1u;
+                } else {  // sub-block 4*lc + w (16 weights)
+                    idx = ((sc >> (4 * w)) & 15u) - 8u;
+                    alpha = (ab >> (4 * (lc % 2) + w)) & 1u;
+                }
+                const float dl = d * float(int(idx));
+                const float v0 = alpha ? -26.f : -31.f, v1 = alpha ? -8.f : -13.f;
+                const float v2 = alpha ? 6.f : 1.f, v3 = alpha ? 22.f : 17.f;
+                const Pool p = make_pool(dl * v0, dl * v1, dl * v2, dl * v3);
+                expand_word(q[w], p, out + 8 * w);
+            }
+        }
+    } else {
+        const uint2_t q = *reinterpret_cast<const uint2_t *>(static_cast<const uint32_t *>(a.s0) + row * (N / 32) + 2 * lc);
+        const uint32_t hb = *reinterpret_cast<const uint32_t *>(static_cast<const uint16_t *>(a.s1) + row * (N / 32) + 2 * lc);
+        const uint32_t dvb = static_cast<const uint16_t *>(a.s2)[row];
+        if constexpr (FLOOR) {
+            const uint32_t iacc = q.x + 3u * q.y + 59u * hb + 67u * dvb;
+            const uint32_t hv = float_to_half_bits(float(iacc & 0xffu));
+#pragma unroll
+            for (int i = 0; i < 32; ++i) out[i] = hv | (hv << 16);
+        } else {
+            const float d = half_bits_to_float(dvb);
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const uint32_t qw = b ? q.y : q.x;
+                const uint32_t h = (hb >> (16 * b)) & 0xffffu;
+                const float dl = d * float(int(2 * ((h >> 12) & 7u) + 1));
+                const float sh = (h & 0x8000u) ? -0.125f : 0.125f;
+                // grid field f in {0,1,2} decodes to f - 1; field 3 never occurs
+                const Pool p = make_pool(dl * (-1.f + sh), dl * (0.f + sh), dl * (1.f + sh), dl * (2.f + sh));
+                const uint32_t c0 = grid[(qw & 0xffu) | ((h & 7u) << 8)];
+                const uint32_t c1 = grid[((qw >> 8) & 0xffu) | (((h >> 3) & 7u) << 8)];
+                const uint32_t c2 = grid[((qw >> 16) & 0xffu) | (((h >> 6) & 7u) << 8)];
+                const uint32_t c3 = grid[(qw >> 24) | (((h >> 9) & 7u) << 8)];
+                expand_word(c0 | (c1 << 16), p, out + 16 * b);
+                expand_word(c2 | (c3 << 16), p, out + 16 * b + 8);
+            }
+        }
+    }
+    uint4_t *d4 = reinterpret_cast<uint4_t *>(dst);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) d4[i] = uint4_t{out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]};
+}
+
+template <int MEMBER, bool FLOOR>
+int launch_dequant(int64_t n, const DequantArgs &a, hipStream_t st) {
+    const uint64_t threads = uint64_t(a.num_experts) * a.out_features * uint64_t(n / 64);
+    const uint64_t blocks = (threads + 255) / 256;
+    if (blocks > 0x7fffffffull) return IQK_ERR_GEOMETRY;
+    const dim3 grid{uint32_t(blocks)}, block{256};
+    if (n == 4096)
+        hipLaunchKernelGGL((dequant_kernel<MEMBER, 4096, FLOOR>), grid, block, 0, st, a);
+    else
+        hipLaunchKernelGGL((dequant_kernel<MEMBER, 2048, FLOOR>), grid, block, 0, st, a);
+    return record_launch(hipGetLastError());
+}
+
+template <bool FLOOR>
+int dequant_entry(int member, int64_t n, int64_t out, int64_t num_experts, const void *const *streams,
+                  int n_streams, const int32_t *slot_of_expert, int64_t n_slots, void *w, void *stream) {
+    const int g = iqk_check_dequant_geometry(member, n, out);
+    if (g != IQK_OK) return g;
+    if (!w || !streams_ok(streams, n_streams, member)) return IQK_ERR_ARGUMENT;
+    if (num_experts <= 0 || num_experts > 0xffffffffll || n_slots < 0 || n_slots > 0xffffffffll)
+        return IQK_ERR_ARGUMENT;
+    if (!slot_of_expert && n_slots < num_experts) return IQK_ERR_ARGUMENT;
+    if (n_slots == 0) return IQK_OK;
+    DequantArgs a;
+    a.s0 = streams[0]; a.s1 = streams[1]; a.s2 = streams[2];
+    a.s3 = n_streams > 3 ? streams[3] : nullptr;
+    a.s4 = n_streams > 4 ? streams[4] : nullptr;
+    a.slot_of_expert = slot_of_expert;
+    a.num_experts = uint32_t(num_experts);
+    a.out_features = uint32_t(out);
+    a.n_slots = uint32_t(n_slots);
+    a.w = static_cast<uint16_t *>(w);
+    hipStream_t st = as_stream(stream);
+    switch (member) {
+        case IQK_MEMBER_IQ2_KS: return launch_dequant<IQ2_KS, FLOOR>(n, a, st);
+        case IQK_MEMBER_IQ2_K: return launch_dequant<IQ2_K, FLOOR>(n, a, st);
+        default: return launch_dequant<IQ1_S_R4, FLOOR>(n, a, st);
+    }
+}
+
+}  // namespace iqk
+
+extern "C" {
+
+int iqk_check_dequant_geometry(int member, int64_t n, int64_t out) {
+    if (!iqk::member_ok(member)) return IQK_ERR_MEMBER;
+    if (!iqk::width_sized(n)) return IQK_ERR_GEOMETRY;
+    if (out <= 0 || out > (int64_t(1) << 24)) return IQK_ERR_GEOMETRY;
+    return IQK_OK;
+}
+
+int iqk_dequant(int member, int64_t n, int64_t out, int64_t num_experts, const void *const *streams,
+                int n_streams, const int32_t *slot_of_expert, int64_t n_slots, void *w, void *stream) {
+    return iqk::dequant_entry<false>(member, n, out, num_experts, streams, n_streams, slot_of_expert, n_slots,
+                                     w, stream);
+}
+
+int iqk_dequant_floor(int member, int64_t n, int64_t out, int64_t num_experts, const void *const *streams,
+                      int n_streams, const int32_t *slot_of_expert, int64_t n_slots, void *w, void *stream) {
+    return iqk::dequant_entry<true>(member, n, out, num_experts, streams, n_streams, slot_of_expert, n_slots,
+                                    w, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,95 @@
+"""ctypes bindings to ``libiqk_hip.so``, the gfx950 kernel library.
+
+Loading never falls back to anything: a missing or stale library raises
+:class:`IqkNativeError`, so no code path can silently compute on the CPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_int, c_int64, c_uint32, c_void_p
+from pathlib import Path
+
+from .build import HIP_LIB
+
+ABI_VERSION = 1
+
+OK, ERR_MEMBER, ERR_GEOMETRY, ERR_ARGUMENT, ERR_LAUNCH = 0, 1, 2, 3, 4
+_CODES = {ERR_MEMBER: "unknown member", ERR_GEOMETRY: "unsized geometry",
+          ERR_ARGUMENT: "bad argument", ERR_LAUNCH: "kernel launch failed"}
+
+MEMBER_IDS = {"iq2_ks": 0, "iq2_k": 1, "iq1_s_r4": 2}
+
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+
+# name -> (restype, argtypes); the declarations of include/iqk_hip.h
+SIGNATURES = {
+    "iqk_hip_abi_version": (c_int, []),
+    "iqk_hip_last_error": (c_int, []),
+    "iqk_check_gemv_geometry": (c_int, [c_int, c_int64, c_int64]),
+    "iqk_check_dequant_geometry": (c_int, [c_int, c_int64, c_int64]),
+    "iqk_gemv": (c_int, [c_int, c_int64, c_int64, c_int64, c_void_p, ctypes.POINTER(c_void_p), c_int,
+                         c_void_p, c_uint32, c_uint32, c_void_p, c_void_p]),
+    "iqk_gemv_floor": (c_int, [c_int, c_int64, c_int64, c_int64, c_void_p, ctypes.POINTER(c_void_p), c_int,
+                               c_void_p, c_uint32, c_uint32, c_void_p, c_void_p]),
+    "iqk_dequant": (c_int, [c_int, c_int64, c_int64, c_int64, ctypes.POINTER(c_void_p), c_int,
+                            c_void_p, c_int64, c_void_p, c_void_p]),
+    "iqk_dequant_floor": (c_int, [c_int, c_int64, c_int64, c_int64, ctypes.POINTER(c_void_p), c_int,
+                                  c_void_p, c_int64, c_void_p, c_void_p]),
+    "iqk_grouped_gemm": (c_int, [c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p,
+                                 c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+}
+
+
+class IqkNativeError(RuntimeError):
+    pass
+
+
+_LIB = None
+
+
+def library_path() -> Path:
+    return HIP_LIB
+
+
+def load() -> ctypes.CDLL:
+    """Load the kernel library (once per process); raise if it is absent."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    path = library_path()
+    if not path.is_file():
+        raise IqkNativeError(
+            f"{path} is not built; run `python -m mlx_iqk_amd.build` (hipcc, gfx950)")
+    lib = ctypes.CDLL(str(path))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    if lib.iqk_hip_abi_version() != ABI_VERSION:
+        raise IqkNativeError(
+            f"{path} has ABI {lib.iqk_hip_abi_version()}, this package expects {ABI_VERSION}; rebuild it")
+    _LIB = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raise on a non-zero ABI return code."""
+    if rc == OK:
+        return
+    detail = _CODES.get(rc, f"code {rc}")
+    if rc == ERR_LAUNCH:
+        detail += f" (hipError {load().iqk_hip_last_error()})"
+    raise IqkNativeError(f"{what}: {detail}")
+
+
+def pointer_array(ptrs) -> ctypes.Array:
+    arr = (c_void_p * len(ptrs))()
+    for i, p in enumerate(ptrs):
+        arr[i] = p
+    return arr
+
+
+__all__ = ["ABI_VERSION", "MEMBER_IDS", "SIGNATURES", "IqkNativeError", "check", "library_path",
+           "load", "pointer_array"]

@@ -1,0 +1,237 @@
+"""Launch wrappers over the gfx950 kernel library, and their geometry guards.
+
+The reference builds Metal source per geometry and dispatches it through
+``mx.fast.metal_kernel`` (src/mlx_iqk/kernels.py:751-887).  Here the kernels
+are compiled once into ``libiqk_hip.so``; these wrappers check every tensor
+against the geometry on the host, then call the C ABI asynchronously on the
+current torch stream.  Nothing here falls back to the CPU: a missing library
+raises.
+
+Guards mirror the reference's (src/mlx_iqk/kernels.py:100-142): the decode
+GEMV and the producer are sized for input widths 2048 and 4096, the GEMV for
+``out_features`` multiples of 16; a width the kernels are not sized for is
+refused before anything launches.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native
+from .format import MEMBERS, check_member, check_row_width, component_dtypes, component_shapes
+
+IQ2_MEMBERS = ("iq2_ks", "iq2_k")
+ROWS_PER_TG = 16
+"""Output rows one decode wavefront produces."""
+WEIGHTS_PER_LANE = 64
+"""Reduction-axis weights each lane of a decode wavefront covers."""
+SUPPORTED_IN_FEATURES = (2048, 4096)
+DEQUANT_THREADS = 256
+TABLE_INPUT_NAMES = {"iq2_ks": "vtab", "iq2_k": "vtab", "iq1_s_r4": "grid"}
+GROUPED_GEMM_N_TILE = 256
+"""out_features granularity of the grouped GEMM."""
+
+
+class IqkKernelError(RuntimeError):
+    pass
+
+
+def check_gemv_geometry(in_features: int, out_features: int) -> tuple[int, int]:
+    n = check_row_width(in_features)
+    if n not in SUPPORTED_IN_FEATURES:
+        raise IqkKernelError(
+            f"the decode gemv is sized per input width and covers {SUPPORTED_IN_FEATURES}, got {in_features}")
+    out = int(out_features)
+    if out <= 0 or out % ROWS_PER_TG:
+        raise IqkKernelError(f"out_features {out_features} is not a positive multiple of {ROWS_PER_TG}")
+    return n, out
+
+
+def check_dequant_geometry(in_features: int, out_features: int) -> tuple[int, int]:
+    n = check_row_width(in_features)
+    if n not in SUPPORTED_IN_FEATURES:
+        raise IqkKernelError(
+            f"the dequantization is sized per input width and covers {SUPPORTED_IN_FEATURES}, got {in_features}")
+    out = int(out_features)
+    if out <= 0:
+        raise IqkKernelError(f"out_features {out_features} is not positive")
+    return n, out
+
+
+def gemv_input_names(member: str) -> list[str]:
+    """Input order of a member's decode GEMV (reference: src/mlx_iqk/kernels.py:751-789)."""
+    check_member(member)
+    return ["x"] + list(component_shapes(member, 1, 1, 2048)) + [TABLE_INPUT_NAMES[member], "sel", "dims"]
+
+
+def dequant_input_names(member: str) -> list[str]:
+    return [n for n in gemv_input_names(member) if n not in ("x", "sel", "dims")]
+
+
+_TORCH_DTYPES = {"uint8": torch.uint8, "uint16": torch.uint16, "uint32": torch.uint32,
+                 "float16": torch.float16}
+
+
+def stream_dtypes(member: str) -> dict[str, torch.dtype]:
+    return {k: _TORCH_DTYPES[v.name] for k, v in component_dtypes(member).items()}
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_cuda(t: torch.Tensor, name: str, dtype: torch.dtype | tuple, device=None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise IqkKernelError(f"{name} must be a torch tensor")
+    if t.device.type != "cuda":
+        raise IqkKernelError(f"{name} must live on a GPU, got {t.device}")
+    if device is not None and t.device != device:
+        raise IqkKernelError(f"{name} is on {t.device}, expected {device}")
+    dts = dtype if isinstance(dtype, tuple) else (dtype,)
+    if t.dtype not in dts:
+        raise IqkKernelError(f"{name} must be {dts}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise IqkKernelError(f"{name} must be contiguous")
+
+
+def check_streams(member: str, streams: list[torch.Tensor], num_experts: int, out_features: int,
+                  in_features: int) -> torch.device:
+    shapes = component_shapes(member, num_experts, out_features, in_features)
+    dtypes = stream_dtypes(member)
+    if len(streams) != len(shapes):
+        raise IqkKernelError(f"{member} needs {len(shapes)} streams, got {len(streams)}")
+    device = streams[0].device
+    for (name, shape), t in zip(shapes.items(), streams):
+        _require_cuda(t, f"stream {name}", dtypes[name], device)
+        if tuple(t.shape) != shape:
+            raise IqkKernelError(f"stream {name} must be {shape}, got {tuple(t.shape)}")
+    return device
+
+
+def gemv(member: str, x: torch.Tensor, streams: list[torch.Tensor], sel: torch.Tensor, pairs_per_row: int,
+         num_experts: int, out_features: int, *, floor: bool = False,
+         out: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode GEMV: ``y[m] = W[sel[m]] @ x[m // pairs_per_row]``, fp16 ``[mats, out]``.
+
+    ``x`` is fp16 ``[rows, in]``, ``sel`` int32/uint32 ``[mats]`` on the same
+    GPU.  ``floor=True`` runs the deleted-decode floor instead.
+    """
+    check_member(member)
+    n = int(x.shape[-1])
+    check_gemv_geometry(n, out_features)
+    device = check_streams(member, streams, num_experts, out_features, n)
+    _require_cuda(x, "x", torch.float16, device)
+    _require_cuda(sel, "sel", (torch.int32, torch.uint32), device)
+    if x.dim() != 2 or sel.dim() != 1:
+        raise IqkKernelError("x must be [rows, in_features] and sel [mats]")
+    mats = int(sel.numel())
+    rows = int(x.shape[0])
+    if pairs_per_row <= 0 or rows * pairs_per_row != mats:
+        raise IqkKernelError(f"{mats} pairs do not tile {rows} activation rows at {pairs_per_row} per row")
+    if out is None:
+        out = torch.empty((mats, out_features), dtype=torch.float16, device=device)
+    else:
+        _require_cuda(out, "out", torch.float16, device)
+        if tuple(out.shape) != (mats, out_features):
+            raise IqkKernelError(f"out must be {(mats, out_features)}, got {tuple(out.shape)}")
+    if mats == 0:
+        return out
+    lib = _native.load()
+    fn = lib.iqk_gemv_floor if floor else lib.iqk_gemv
+    ptrs = _native.pointer_array([t.data_ptr() for t in streams])
+    # gridDim.y carries the pair index: launch in pair chunks that keep whole
+    # activation rows together.
+    limit = (65535 // pairs_per_row) * pairs_per_row
+    stream = _stream_ptr(device)
+    for m0 in range(0, mats, limit):
+        cnt = min(limit, mats - m0)
+        rc = fn(_native.MEMBER_IDS[member], n, out_features, num_experts,
+                x.data_ptr() + (m0 // pairs_per_row) * n * 2, ptrs, len(streams),
+                sel.data_ptr() + 4 * m0, pairs_per_row, cnt, out.data_ptr() + m0 * out_features * 2, stream)
+        _native.check(rc, f"iqk_gemv{'_floor' if floor else ''}({member}, {n}x{out_features})")
+    return out
+
+
+def dequant(member: str, streams: list[torch.Tensor], num_experts: int, out_features: int, in_features: int,
+            *, slot_of_expert: torch.Tensor | None = None, n_slots: int | None = None, floor: bool = False,
+            out: torch.Tensor | None = None) -> torch.Tensor:
+    """Producer: fp16 ``[n_slots, out, in]``, slot ``slot_of_expert[e]`` <- expert ``e``.
+
+    Without ``slot_of_expert`` every expert lands in its own slot.  Slots no
+    expert maps to are left unwritten.
+    """
+    check_member(member)
+    check_dequant_geometry(in_features, out_features)
+    device = check_streams(member, streams, num_experts, out_features, in_features)
+    if slot_of_expert is None:
+        n_slots = num_experts if n_slots is None else int(n_slots)
+        if n_slots < num_experts:
+            raise IqkKernelError("without slot_of_expert every expert needs its own slot")
+        slot_ptr = None
+    else:
+        _require_cuda(slot_of_expert, "slot_of_expert", torch.int32, device)
+        if tuple(slot_of_expert.shape) != (num_experts,):
+            raise IqkKernelError(f"slot_of_expert must be [{num_experts}]")
+        if n_slots is None:
+            raise IqkKernelError("n_slots is required with slot_of_expert")
+        slot_ptr = slot_of_expert.data_ptr()
+    shape = (int(n_slots), out_features, in_features)
+    if out is None:
+        out = torch.empty(shape, dtype=torch.float16, device=device)
+    else:
+        _require_cuda(out, "out", torch.float16, device)
+        if tuple(out.shape) != shape:
+            raise IqkKernelError(f"out must be {shape}, got {tuple(out.shape)}")
+    lib = _native.load()
+    fn = lib.iqk_dequant_floor if floor else lib.iqk_dequant
+    ptrs = _native.pointer_array([t.data_ptr() for t in streams])
+    rc = fn(_native.MEMBER_IDS[member], in_features, out_features, num_experts, ptrs, len(streams),
+            slot_ptr, int(n_slots), out.data_ptr(), _stream_ptr(device))
+    _native.check(rc, f"iqk_dequant{'_floor' if floor else ''}({member}, {in_features}x{out_features})")
+    return out
+
+
+def grouped_gemm(x: torch.Tensor, w: torch.Tensor, group_offsets: torch.Tensor, x_rows: torch.Tensor,
+                 y_rows: torch.Tensor | None = None, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Sorted grouped GEMM: ``y[y_rows[p]] = x[x_rows[p]] @ w[g(p)]^T`` for slot ``p``.
+
+    ``x`` fp16 ``[rows, K]``; ``w`` fp16 ``[G, N, K]``; ``group_offsets``
+    int32 ``[G + 1]`` (slot ranges, sorted by group); ``x_rows``/``y_rows``
+    int32 ``[P]``.  Returns fp16 ``[P, N]``.
+    """
+    _require_cuda(x, "x", torch.float16)
+    device = x.device
+    _require_cuda(w, "w", torch.float16, device)
+    _require_cuda(group_offsets, "group_offsets", (torch.int32, torch.uint32), device)
+    _require_cuda(x_rows, "x_rows", (torch.int32, torch.uint32), device)
+    if x.dim() != 2 or w.dim() != 3 or w.shape[2] != x.shape[1]:
+        raise IqkKernelError(f"x [rows, K] and w [G, N, K] disagree: {tuple(x.shape)} vs {tuple(w.shape)}")
+    G, N, K = (int(s) for s in w.shape)
+    P = int(x_rows.numel())
+    if tuple(group_offsets.shape) != (G + 1,):
+        raise IqkKernelError(f"group_offsets must be [{G + 1}]")
+    if N % GROUPED_GEMM_N_TILE or K % 32:
+        raise IqkKernelError(f"grouped gemm needs N % {GROUPED_GEMM_N_TILE} == 0 and K % 32 == 0")
+    if y_rows is not None:
+        _require_cuda(y_rows, "y_rows", (torch.int32, torch.uint32), device)
+        if y_rows.numel() != P:
+            raise IqkKernelError("y_rows and x_rows must have the same length")
+    if out is None:
+        out = torch.empty((P, N), dtype=torch.float16, device=device)
+    else:
+        _require_cuda(out, "out", torch.float16, device)
+        if tuple(out.shape) != (P, N):
+            raise IqkKernelError(f"out must be {(P, N)}")
+    rc = _native.load().iqk_grouped_gemm(
+        K, N, G, P, x.data_ptr(), int(x.shape[0]), w.data_ptr(), group_offsets.data_ptr(), x_rows.data_ptr(),
+        y_rows.data_ptr() if y_rows is not None else None, out.data_ptr(), _stream_ptr(device))
+    _native.check(rc, f"iqk_grouped_gemm(K={K}, N={N}, G={G}, P={P})")
+    return out
+
+
+__all__ = [
+    "DEQUANT_THREADS", "GROUPED_GEMM_N_TILE", "IQ2_MEMBERS", "MEMBERS", "ROWS_PER_TG",
+    "SUPPORTED_IN_FEATURES", "TABLE_INPUT_NAMES", "WEIGHTS_PER_LANE", "IqkKernelError",
+    "check_dequant_geometry", "check_gemv_geometry", "check_streams", "dequant", "dequant_input_names",
+    "gemv", "gemv_input_names", "grouped_gemm", "stream_dtypes",
+]

@@ -1,0 +1,208 @@
+"""Stacked-expert IQ_K module with the ``(x, indices, sorted_indices)`` switch interface.
+
+The drop-in for the reference's ``IqkSwitchLinear`` (src/mlx_iqk/nn.py:105-333)
+on PyTorch-ROCm: same constructor, same stream contract (the relayout
+streams are module buffers named and shaped by the format), same call seam,
+same route choice (src/mlx_iqk/nn.py:49, 221-238):
+
+* **decode** (``indices.numel() <= DECODE_MAT_LIMIT`` and not sorted): the
+  fused GEMV streams the selected experts' relayout directly;
+* **prefill** (otherwise): the producer reconstructs each routed expert once,
+  bit-exact, into fp16, and a sorted grouped fp16 MFMA GEMM contracts it.
+  The reference dequantizes every expert and calls ``mx.gather_mm``; here
+  only the routed experts are reconstructed, and the pair sort, grouping and
+  un-permute happen on the device with no host synchronisation.
+
+Shapes follow the reference: gate/up pass ``x [..., 1, 1, in]`` (one row per
+token shared by its ``top_k`` experts), down passes ``x [..., top_k, 1, in]``
+(one row per pair); ``indices`` is ``[..., top_k]``; the result is
+``[..., top_k, 1, out]``.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from . import kernels
+from .format import IQ2NL_VALUES, check_member, component_shapes
+from .iq1grid import grid_values
+from .kernels import IqkKernelError, check_dequant_geometry, check_gemv_geometry, stream_dtypes
+
+DECODE_MAT_LIMIT = 63
+"""Token-expert pairs at or below which the decode GEMV serves
+(reference: src/mlx_iqk/nn.py:49-54)."""
+
+
+class IqkRuntimeError(RuntimeError):
+    pass
+
+
+_TABLES: dict[tuple, torch.Tensor] = {}
+
+
+def value_table(device=None) -> torch.Tensor:
+    """The fp16 ``iq2nl_values`` table, one shared tensor per device.
+
+    The kernels carry the same eight values compiled in; this is the table's
+    host-visible form (reference: src/mlx_iqk/nn.py:60-71).
+    """
+    key = ("vtab", str(torch.device(device) if device is not None else "cpu"))
+    if key not in _TABLES:
+        _TABLES[key] = torch.from_numpy(IQ2NL_VALUES.astype(np.float16)).to(device or "cpu")
+    return _TABLES[key]
+
+
+def grid_table(device=None) -> torch.Tensor:
+    """The IQ1_S grid values as 4096 little-endian uint32 words, two per entry
+    (reference: src/mlx_iqk/nn.py:74-88)."""
+    key = ("grid", str(torch.device(device) if device is not None else "cpu"))
+    if key not in _TABLES:
+        words = np.ascontiguousarray(grid_values()).view(np.uint32).reshape(-1).copy()
+        _TABLES[key] = torch.from_numpy(words).to(device or "cpu")
+    return _TABLES[key]
+
+
+def member_table(member: str, device=None) -> torch.Tensor:
+    check_member(member)
+    return grid_table(device) if member == "iq1_s_r4" else value_table(device)
+
+
+class IqkSwitchLinear(torch.nn.Module):
+    """Stacked IQ_K experts for one projection, ``(x, indices)`` interface."""
+
+    mode = "iqk"
+
+    def __init__(self, member: str, num_experts: int, out_features: int, in_features: int,
+                 device=None):
+        super().__init__()
+        self.member = check_member(member)
+        check_gemv_geometry(in_features, out_features)
+        check_dequant_geometry(in_features, out_features)
+        self.num_experts = int(num_experts)
+        self.out_features = int(out_features)
+        self.in_features = int(in_features)
+        if self.num_experts <= 0:
+            raise IqkRuntimeError(f"num_experts {num_experts} is not positive")
+        dtypes = stream_dtypes(member)
+        for name, shape in component_shapes(member, num_experts, out_features, in_features).items():
+            self.register_buffer(name, torch.zeros(shape, dtype=dtypes[name], device=device))
+
+    # -- wire streams -------------------------------------------------------
+
+    def stream_names(self) -> list[str]:
+        """Relayout stream names of this member, in kernel input order."""
+        return list(component_shapes(self.member, self.num_experts, self.out_features, self.in_features))
+
+    def _streams(self) -> list[torch.Tensor]:
+        return [getattr(self, name) for name in self.stream_names()]
+
+    def load_streams(self, streams: dict) -> None:
+        """Install packed streams (numpy arrays or tensors), checking every shape.
+
+        Arrays land on the module's device with the format's dtypes; a
+        missing, extra or misshapen stream is refused
+        (reference: src/mlx_iqk/nn.py:137-151).
+        """
+        shapes = component_shapes(self.member, self.num_experts, self.out_features, self.in_features)
+        if set(streams) != set(shapes):
+            raise IqkRuntimeError(f"{self.member} needs streams {sorted(shapes)}, got {sorted(streams)}")
+        dtypes = stream_dtypes(self.member)
+        staged = {}
+        for name, want in shapes.items():
+            value = streams[name]
+            if isinstance(value, np.ndarray):
+                value = torch.from_numpy(np.ascontiguousarray(value))
+            got = tuple(value.shape)
+            if got != want:
+                raise IqkRuntimeError(
+                    f"stream {name} must be {want} for "
+                    f"{self.num_experts}x{self.out_features}x{self.in_features}, got {got}")
+            if value.dtype != dtypes[name]:
+                raise IqkRuntimeError(f"stream {name} must be {dtypes[name]}, got {value.dtype}")
+            staged[name] = value
+        device = getattr(self, "qs").device
+        for name, value in staged.items():
+            setattr(self, name, value.to(device).contiguous())
+
+    # -- dequantized route (prefill) -----------------------------------------
+
+    def dequantized(self) -> torch.Tensor:
+        """Full fp16 dequantization ``[E, out, in]``, bit-identical to the CPU decode
+        (reference: src/mlx_iqk/nn.py:155-169)."""
+        return kernels.dequant(self.member, self._streams(), self.num_experts, self.out_features,
+                               self.in_features)
+
+    def dequantized_experts(self, slot_of_expert: torch.Tensor, n_slots: int) -> torch.Tensor:
+        """fp16 ``[n_slots, out, in]`` holding expert ``e`` in slot ``slot_of_expert[e]``."""
+        return kernels.dequant(self.member, self._streams(), self.num_experts, self.out_features,
+                               self.in_features, slot_of_expert=slot_of_expert, n_slots=n_slots)
+
+    # -- call -------------------------------------------------------------------
+
+    def forward(self, x: torch.Tensor, indices: torch.Tensor, sorted_indices: bool = False) -> torch.Tensor:
+        """Project ``x`` through the experts named by ``indices`` (route as the reference)."""
+        if indices.numel() <= DECODE_MAT_LIMIT and not sorted_indices:
+            return self.gemv(x, indices)
+        return self.prefill(x, indices)
+
+    def gemv(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        """Fused GEMV over the selected experts; valid for any pair count
+        (reference: src/mlx_iqk/nn.py:240-271)."""
+        xt = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
+        sel = indices.reshape(-1).to(torch.int32).contiguous()
+        mats, rows = int(sel.numel()), int(xt.shape[0])
+        # Pairs sharing one activation row: top_k for gate/up, 1 for down.
+        if rows <= 0 or mats % rows:
+            raise IqkRuntimeError(
+                f"{mats} token-expert pairs do not tile {rows} activation row(s); "
+                "the operand and the routing disagree")
+        out = kernels.gemv(self.member, xt, self._streams(), sel, mats // rows, self.num_experts,
+                           self.out_features)
+        return out.reshape(list(indices.shape) + [self.out_features]).unsqueeze(-2)
+
+    def prefill(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        """Producer + sorted grouped GEMM; the dequantized route of ``forward``.
+
+        Broadcasting follows ``gather_mm(x, W^T, rhs_indices=indices)``: the
+        batch shape is ``broadcast(x.shape[:-2], indices.shape)`` and each pair
+        contracts its ``x.shape[-2]`` rows.
+        """
+        if x.shape[-1] != self.in_features or x.dim() < 2:
+            raise IqkRuntimeError(f"x must be [..., M, {self.in_features}], got {tuple(x.shape)}")
+        device = self.qs.device
+        xb = x.to(torch.float16)
+        M = int(xb.shape[-2])
+        batch = torch.broadcast_shapes(tuple(xb.shape[:-2]), tuple(indices.shape))
+        P = math.prod(batch)
+        if P == 0:
+            return torch.empty(tuple(batch) + (M, self.out_features), dtype=torch.float16, device=device)
+        xbatch = tuple(xb.shape[:-2])
+        xflat = xb.reshape(-1, self.in_features).contiguous()
+        xidx = torch.arange(math.prod(xbatch), device=device).reshape(xbatch).broadcast_to(batch).reshape(-1)
+        ids = indices.to(device=device, dtype=torch.int64).broadcast_to(batch).reshape(-1)
+        # Experts are routed only if some pair names them; compact them into
+        # slots in expert order.  n_slots is an upper bound known on the host.
+        E = self.num_experts
+        present = torch.zeros(E, dtype=torch.int32, device=device).index_fill_(0, ids, 1)
+        slot_of_expert = torch.where(present > 0, torch.cumsum(present, 0, dtype=torch.int32) - 1,
+                                     torch.full_like(present, -1))
+        n_slots = min(E, P)
+        order = torch.argsort(ids, stable=True)
+        slot_of_pair = slot_of_expert[ids].to(torch.int64)
+        counts = torch.zeros(n_slots, dtype=torch.int64, device=device).index_add_(
+            0, slot_of_pair, torch.full_like(slot_of_pair, M))
+        offsets = torch.zeros(n_slots + 1, dtype=torch.int32, device=device)
+        offsets[1:] = torch.cumsum(counts, 0).to(torch.int32)
+        r = torch.arange(M, device=device)
+        x_rows = (xidx[order][:, None] * M + r).reshape(-1).to(torch.int32)
+        y_rows = (order[:, None] * M + r).reshape(-1).to(torch.int32)
+        w = self.dequantized_experts(slot_of_expert, n_slots)
+        y = kernels.grouped_gemm(xflat, w, offsets, x_rows, y_rows)
+        return y.reshape(tuple(batch) + (M, self.out_features))
+
+
+__all__ = ["DECODE_MAT_LIMIT", "IqkKernelError", "IqkRuntimeError", "IqkSwitchLinear", "grid_table",
+           "member_table", "value_table"]

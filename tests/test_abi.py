@@ -1,0 +1,93 @@
+"""The C ABI's host-side contract, checked without a GPU.
+
+* every function include/iqk_hip.h and include/iqk_codec.h declare is exported
+  by the built library, with the ctypes signature the package binds;
+* the geometry guards refuse what the reference refuses
+  (src/mlx_iqk/kernels.py:100-142) and accept the routed geometry;
+* every entry point refuses a bad argument before any HIP call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from mlx_iqk_amd import _native, build, codec
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared(header: Path) -> set[str]:
+    text = re.sub(r"//[^\n]*", "", header.read_text())
+    return set(re.findall(r"\b(iqk_[a-z0-9_]+)\s*\(", text))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not build.HIP_LIB.is_file():
+        build.build_hip()
+    return _native.load()
+
+
+def test_every_declared_kernel_entry_point_is_exported_and_bound(lib):
+    declared = _declared(ROOT / "include" / "iqk_hip.h")
+    assert declared == set(_native.SIGNATURES)
+    for name in declared:
+        assert getattr(lib, name) is not None
+
+
+def test_every_declared_codec_entry_point_is_exported():
+    declared = _declared(ROOT / "include" / "iqk_codec.h")
+    lib = codec.load()
+    for name in declared:
+        assert getattr(lib, name) is not None, name
+
+
+def test_abi_version(lib):
+    assert lib.iqk_hip_abi_version() == _native.ABI_VERSION
+
+
+@pytest.mark.parametrize("member", (0, 1, 2))
+def test_geometry_guards(lib, member):
+    for n in (2048, 4096):
+        assert lib.iqk_check_gemv_geometry(member, n, 2048) == 0
+        assert lib.iqk_check_dequant_geometry(member, n, 4096) == 0
+    for bad_n in (1024, 1536, 2560, 3072, 4352, 8192, 0, -2048):
+        assert lib.iqk_check_gemv_geometry(member, bad_n, 32) == _native.ERR_GEOMETRY
+        assert lib.iqk_check_dequant_geometry(member, bad_n, 32) == _native.ERR_GEOMETRY
+    for bad_out in (24, 40, 100, 0, -16):
+        assert lib.iqk_check_gemv_geometry(member, 2048, bad_out) == _native.ERR_GEOMETRY
+    assert lib.iqk_check_dequant_geometry(member, 2048, 24) == 0  # the producer takes any row count
+    assert lib.iqk_check_gemv_geometry(3, 2048, 32) == _native.ERR_MEMBER
+
+
+def test_entry_points_refuse_bad_arguments_before_launching(lib):
+    p = ctypes.c_void_p(16)  # never dereferenced: every call below is refused first
+    streams = _native.pointer_array([16] * 5)
+    # wrong stream count, null x, null output, pairs not tiling rows, bad member
+    assert lib.iqk_gemv(0, 4096, 2048, 256, p, streams, 4, p, 6, 12, p, None) == _native.ERR_ARGUMENT
+    assert lib.iqk_gemv(0, 4096, 2048, 256, None, streams, 5, p, 6, 12, p, None) == _native.ERR_ARGUMENT
+    assert lib.iqk_gemv(0, 4096, 2048, 256, p, streams, 5, p, 6, 12, None, None) == _native.ERR_ARGUMENT
+    assert lib.iqk_gemv(0, 4096, 2048, 256, p, streams, 5, p, 5, 12, p, None) == _native.ERR_ARGUMENT
+    assert lib.iqk_gemv(7, 4096, 2048, 256, p, streams, 5, p, 6, 12, p, None) == _native.ERR_MEMBER
+    assert lib.iqk_gemv_floor(1, 3072, 2048, 256, p, streams, 4, p, 6, 12, p, None) == _native.ERR_GEOMETRY
+    assert lib.iqk_dequant(2, 2048, 32, 4, streams, 5, None, 4, p, None) == _native.ERR_ARGUMENT
+    assert lib.iqk_dequant(2, 2048, 32, 4, streams, 3, None, 2, p, None) == _native.ERR_ARGUMENT
+    assert lib.iqk_dequant_floor(0, 2048, 32, 0, streams, 5, None, 4, p, None) == _native.ERR_ARGUMENT
+    assert lib.iqk_grouped_gemm(4096, 2000, 4, 8, p, 8, p, p, p, None, p, None) == _native.ERR_GEOMETRY
+    assert lib.iqk_grouped_gemm(4020, 2048, 4, 8, p, 8, p, p, p, None, p, None) == _native.ERR_GEOMETRY
+    assert lib.iqk_grouped_gemm(4096, 2048, 4, 8, None, 8, p, p, p, None, p, None) == _native.ERR_ARGUMENT
+    # empty work is a no-op success, with no launch
+    assert lib.iqk_gemv(0, 4096, 2048, 256, p, streams, 5, p, 6, 0, p, None) == 0
+    assert lib.iqk_grouped_gemm(4096, 2048, 0, 0, None, 0, None, None, None, None, None, None) == 0
+    assert lib.iqk_hip_last_error() == 0
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_native, "_LIB", None)
+    monkeypatch.setattr(_native, "library_path", lambda: tmp_path / "absent.so")
+    with pytest.raises(_native.IqkNativeError):
+        _native.load()

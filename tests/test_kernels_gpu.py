@@ -1,0 +1,204 @@
+"""GPU parity of the HIP kernels through the C ABI, against the oracle.
+
+Mirrors the reference's kernel gate (tests/test_kernels.py):
+
+1. the producer is **bit-exact**: its fp16 equals the oracle's float32
+   dequantization rounded to fp16 (round-to-nearest-even), compared on raw
+   bits, over random wire (serving and full-range scales) and converted rows;
+2. the decode GEMV matches a float64 contraction of the oracle's weights:
+   ``max|d| / max|ref| < 1.5e-3``, rel-L2 <= 1e-3 (the stated bar), and more
+   than 99% of outputs at 0 fp16 ULP from the correctly rounded result;
+3. the grouped GEMM matches a float64 contraction of the fp16 weights
+   within the prefill tolerance (3e-3, reference tests/test_nn.py:132).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import wirepack
+from mlx_iqk_amd import codec, kernels
+from mlx_iqk_amd import format as fmt
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+EXPERTS = 4
+OUT = 64
+
+
+def _fp16_ulp(got: np.ndarray, want: np.ndarray) -> np.ndarray:
+    def order(a):
+        i = a.astype(np.float16).view(np.int16).astype(np.int64)
+        return np.where(i < 0, np.int64(-32768) - i, i)
+    return np.abs(order(got) - order(want))
+
+
+def _streams(member, wire, experts, out, n, device):
+    packed = fmt.pack(member, wire, n)
+    shapes = fmt.component_shapes(member, experts, out, n)
+    return [torch.from_numpy(np.ascontiguousarray(packed[k]).reshape(shapes[k])).to(device) for k in shapes]
+
+
+def _case(member, n, seed, device, experts=EXPERTS, out=OUT, scales="serving"):
+    wire = wirepack.random_wire(member, experts * out, n, seed=seed, scales=scales)
+    ref = oracle.dequantize(member, wire, n).reshape(experts, out, n)
+    return wire, _streams(member, wire, experts, out, n, device), ref
+
+
+def _check_gemv(got: np.ndarray, want: np.ndarray, label) -> None:
+    got = got.astype(np.float64)
+    rel = np.max(np.abs(got - want)) / np.max(np.abs(want))
+    l2 = np.linalg.norm(got - want) / np.linalg.norm(want)
+    exact = float(np.mean(_fp16_ulp(got, want.astype(np.float16)) == 0))
+    assert rel < 1.5e-3, (label, rel)
+    assert l2 <= 1e-3, (label, l2)
+    assert exact > 0.99, (label, exact)
+
+
+# -- the producer is bit-exact --------------------------------------------------
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+@pytest.mark.parametrize("n", kernels.SUPPORTED_IN_FEATURES)
+@pytest.mark.parametrize("scales", ("serving", "sweep"))
+def test_dequant_is_bit_identical_to_the_oracle(device, member, n, scales):
+    print(f"dequant {member} n={n} scales={scales}", flush=True)
+    _, streams, ref = _case(member, n, wirepack.seed_for(member, n, scales), device, scales=scales)
+    got = kernels.dequant(member, streams, EXPERTS, OUT, n).cpu().numpy()
+    want = ref.astype(np.float16)
+    bad = int(np.sum(got.view(np.uint16) != want.view(np.uint16)))
+    assert bad == 0, f"{bad} of {got.size} fp16 words differ"
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+@pytest.mark.parametrize("n", kernels.SUPPORTED_IN_FEATURES)
+def test_dequant_is_bit_identical_on_converted_rows(device, member, n):
+    print(f"dequant converted {member} n={n}", flush=True)
+    rng = np.random.default_rng(4242)
+    rows = (rng.standard_normal((EXPERTS * OUT, n)) * 0.02).astype(np.float32)
+    wire = codec.quantize(member, rows, (rng.random(n) * 0.9 + 0.1).astype(np.float32))
+    streams = _streams(member, wire, EXPERTS, OUT, n, device)
+    got = kernels.dequant(member, streams, EXPERTS, OUT, n).cpu().numpy()
+    want = oracle.dequantize(member, wire, n).reshape(EXPERTS, OUT, n).astype(np.float16)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+def test_dequant_writes_selected_experts_into_their_slots(device, member):
+    print(f"dequant slots {member}", flush=True)
+    n, experts = 2048, 6
+    _, streams, ref = _case(member, n, 77, device, experts=experts, out=32)
+    slot = torch.tensor([2, -1, 0, -1, 1, 9], dtype=torch.int32, device=device)  # 9 is out of range: skipped
+    out = torch.full((3, 32, n), 12345, dtype=torch.int16, device=device).view(torch.float16)
+    kernels.dequant(member, streams, experts, 32, n, slot_of_expert=slot, n_slots=3, out=out)
+    got = out.cpu().numpy()
+    for e, s in ((0, 2), (2, 0), (4, 1)):
+        assert np.array_equal(got[s].view(np.uint16), ref[e].astype(np.float16).view(np.uint16)), (e, s)
+
+
+def test_dequant_is_deterministic(device):
+    _, streams, _ = _case("iq2_ks", 4096, 5, device)
+    a = kernels.dequant("iq2_ks", streams, EXPERTS, OUT, 4096)
+    b = kernels.dequant("iq2_ks", streams, EXPERTS, OUT, 4096)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+# -- the decode GEMV ----------------------------------------------------------------
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+@pytest.mark.parametrize("n", kernels.SUPPORTED_IN_FEATURES)
+def test_gemv_matches_a_float64_reference_shared_rows(device, member, n):
+    """The gate/up seam: each token's row is shared by its top_k experts."""
+    print(f"gemv shared {member} n={n}", flush=True)
+    _, streams, ref = _case(member, n, wirepack.seed_for(member, n, "gemv"), device)
+    rng = np.random.default_rng(17)
+    tokens, top_k = 8, 3
+    x = rng.standard_normal((tokens, n)).astype(np.float16)
+    sel = rng.integers(0, EXPERTS, size=tokens * top_k).astype(np.int32)
+    got = kernels.gemv(member, torch.from_numpy(x).to(device), streams, torch.from_numpy(sel).to(device),
+                       top_k, EXPERTS, OUT).cpu().numpy()
+    _check_gemv(got, oracle.gemv_reference(ref, sel, x, top_k), (member, n))
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+@pytest.mark.parametrize("n", kernels.SUPPORTED_IN_FEATURES)
+def test_gemv_matches_a_float64_reference_per_pair_rows(device, member, n):
+    """The down seam: one activation row per pair."""
+    print(f"gemv per-pair {member} n={n}", flush=True)
+    _, streams, ref = _case(member, n, wirepack.seed_for(member, n, "gemv-down"), device)
+    rng = np.random.default_rng(19)
+    pairs = 12
+    x = rng.standard_normal((pairs, n)).astype(np.float16)
+    sel = rng.integers(0, EXPERTS, size=pairs).astype(np.int32)
+    got = kernels.gemv(member, torch.from_numpy(x).to(device), streams, torch.from_numpy(sel).to(device),
+                       1, EXPERTS, OUT).cpu().numpy()
+    _check_gemv(got, oracle.gemv_reference(ref, sel, x, 1), (member, n))
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+def test_gemv_reads_the_expert_the_index_names(device, member):
+    n = 2048
+    _, streams, ref = _case(member, n, 555, device)
+    x = np.random.default_rng(23).standard_normal((1, n)).astype(np.float16)
+    xt = torch.from_numpy(x).to(device)
+    for e in range(EXPERTS):
+        sel = torch.tensor([e], dtype=torch.int32, device=device)
+        got = kernels.gemv(member, xt, streams, sel, 1, EXPERTS, OUT).cpu().numpy()[0].astype(np.float64)
+        want = ref[e].astype(np.float64) @ x[0].astype(np.float64)
+        assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 1.5e-3, e
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+def test_gemv_marks_an_out_of_range_expert_with_nan(device, member):
+    """An id beyond the stack is never dereferenced: its rows come back NaN."""
+    n = 2048
+    _, streams, ref = _case(member, n, 31, device)
+    x = np.random.default_rng(1).standard_normal((3, n)).astype(np.float16)
+    sel = np.array([1, EXPERTS + 5, 2], dtype=np.int32)
+    got = kernels.gemv(member, torch.from_numpy(x).to(device), streams, torch.from_numpy(sel).to(device),
+                       1, EXPERTS, OUT).cpu().numpy()
+    assert np.all(np.isnan(got[1]))
+    ok = oracle.gemv_reference(ref, sel[[0, 2]], x[[0, 2]], 1)
+    _check_gemv(got[[0, 2]], ok, member)
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+@pytest.mark.parametrize("n", kernels.SUPPORTED_IN_FEATURES)
+def test_floor_kernels_run(device, member, n):
+    _, streams, _ = _case(member, n, 9, device)
+    x = torch.randn(2, n, device=device).to(torch.float16)
+    sel = torch.tensor([0, 3, 1, 2], dtype=torch.int32, device=device)
+    y = kernels.gemv(member, x, streams, sel, 2, EXPERTS, OUT, floor=True)
+    w = kernels.dequant(member, streams, EXPERTS, OUT, n, floor=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all() and torch.isfinite(w.float()).all()
+
+
+# -- the grouped GEMM -----------------------------------------------------------------
+
+
+@pytest.mark.parametrize("K,N", [(4096, 2048), (2048, 4096), (2048, 256)])
+def test_grouped_gemm_matches_a_float64_reference(device, K, N):
+    print(f"grouped gemm K={K} N={N}", flush=True)
+    rng = np.random.default_rng(K + N)
+    counts = np.array([0, 1, 70, 5, 0, 130, 17, 64], dtype=np.int64)  # empty, ragged, >1 M-tile
+    G, P = len(counts), int(counts.sum())
+    w = (rng.standard_normal((G, N, K)) * 0.02).astype(np.float16)
+    xrows = 300
+    x = rng.standard_normal((xrows, K)).astype(np.float16)
+    x_rows = rng.integers(0, xrows, size=P).astype(np.int32)
+    y_rows = rng.permutation(P).astype(np.int32)
+    offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    got = kernels.grouped_gemm(torch.from_numpy(x).to(device), torch.from_numpy(w).to(device),
+                               torch.from_numpy(offs).to(device), torch.from_numpy(x_rows).to(device),
+                               torch.from_numpy(y_rows).to(device)).cpu().numpy().astype(np.float64)
+    want = np.empty((P, N))
+    g_of = np.repeat(np.arange(G), counts)
+    for p in range(P):
+        want[y_rows[p]] = x[x_rows[p]].astype(np.float64) @ w[g_of[p]].astype(np.float64).T
+    rel = np.max(np.abs(got - want)) / np.max(np.abs(want))
+    assert rel < 3e-3, rel

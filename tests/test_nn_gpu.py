@@ -1,0 +1,204 @@
+"""The switch module on the GPU: both routes, both seams, mixed members.
+
+Mirrors the reference's module tests (tests/test_nn.py): decode route for
+small dispatches, the sorted prefill route, route agreement, the down-operand
+seam with its anti-case, one layer mixing members.  References are float64
+contractions of the oracle's dequantization.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import wirepack
+from mlx_iqk_amd import format as fmt
+from mlx_iqk_amd.iq1grid import grid_values
+from mlx_iqk_amd.nn import DECODE_MAT_LIMIT, IqkRuntimeError, IqkSwitchLinear, grid_table, member_table, value_table
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+EXPERTS = 8
+OUT = 256
+
+
+def _module(member, n, seed, device, out=OUT, experts=EXPERTS):
+    wire = wirepack.random_wire(member, experts * out, n, seed=seed, scales="serving")
+    streams = fmt.pack(member, wire, n)
+    shapes = fmt.component_shapes(member, experts, out, n)
+    module = IqkSwitchLinear(member, experts, out, n, device=device)
+    module.load_streams({k: np.ascontiguousarray(v).reshape(shapes[k]) for k, v in streams.items()})
+    ref = oracle.dequantize(member, wire, n).reshape(experts, out, n)
+    return module, ref
+
+
+def _rel(got, want):
+    got = got.detach().float().cpu().numpy().astype(np.float64).reshape(want.shape)
+    return np.max(np.abs(got - want)) / np.max(np.abs(want))
+
+
+def test_tables_are_shared_and_exact(device):
+    t = value_table(device)
+    assert t.dtype == torch.float16 and value_table(device) is t
+    assert np.array_equal(t.cpu().numpy().astype(np.int64), fmt.IQ2NL_VALUES.astype(np.int64))
+    g = grid_table(device)
+    assert g.shape == (4096,)
+    assert np.array_equal(g.cpu().numpy().view(np.int8).reshape(2048, 8), grid_values())
+    assert member_table("iq1_s_r4", device) is g and member_table("iq2_k", device) is t
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+def test_load_streams_rejects_wrong_or_missing_streams(device, member):
+    module, _ = _module(member, 2048, 1, device)
+    streams = {k: getattr(module, k) for k in module.stream_names()}
+    bad = dict(streams)
+    bad["qs"] = torch.zeros((EXPERTS, OUT, 3), dtype=torch.uint32, device=device)
+    with pytest.raises(IqkRuntimeError):
+        module.load_streams(bad)
+    missing = dict(streams)
+    missing.pop(module.stream_names()[1])
+    with pytest.raises(IqkRuntimeError):
+        module.load_streams(missing)
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+@pytest.mark.parametrize("n", (2048, 4096))
+def test_decode_route_serves_small_dispatches(device, member, n):
+    print(f"decode route {member} n={n}", flush=True)
+    module, ref = _module(member, n, wirepack.seed_for(member, n), device)
+    rng = np.random.default_rng(31)
+    tokens, top_k = 4, 6
+    assert tokens * top_k <= DECODE_MAT_LIMIT
+    x = rng.standard_normal((tokens, 1, 1, n)).astype(np.float16)
+    idx = rng.integers(0, EXPERTS, size=(tokens, top_k)).astype(np.int32)
+    got = module(torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device))
+    assert tuple(got.shape) == (tokens, top_k, 1, OUT)
+    want = np.stack([[ref[idx[t, k]].astype(np.float64) @ x[t, 0, 0].astype(np.float64)
+                      for k in range(top_k)] for t in range(tokens)])[:, :, None, :]
+    assert _rel(got, want) < 1.5e-3
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+@pytest.mark.parametrize("n", (2048, 4096))
+def test_decode_route_serves_the_down_operand_shape(device, member, n):
+    module, ref = _module(member, n, wirepack.seed_for(member, n, "down"), device)
+    rng = np.random.default_rng(59)
+    tokens, top_k = 4, 4
+    x = rng.standard_normal((tokens, top_k, 1, n)).astype(np.float16)
+    idx = rng.integers(0, EXPERTS, size=(tokens, top_k)).astype(np.int32)
+    got = module(torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device))
+    want = np.stack([[ref[idx[t, k]].astype(np.float64) @ x[t, k, 0].astype(np.float64)
+                      for k in range(top_k)] for t in range(tokens)])[:, :, None, :]
+    assert _rel(got, want) < 1.5e-3
+    # anti-case: a module that read row 0 for every pair would differ
+    shared = np.stack([[ref[idx[t, k]].astype(np.float64) @ x[t, 0, 0].astype(np.float64)
+                        for k in range(top_k)] for t in range(tokens)])[:, :, None, :]
+    assert np.max(np.abs(shared - want)) > 1e-2 * np.max(np.abs(want))
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+@pytest.mark.parametrize("n", (2048, 4096))
+def test_prefill_route_serves_sorted_dispatches(device, member, n):
+    print(f"prefill route {member} n={n}", flush=True)
+    module, ref = _module(member, n, wirepack.seed_for(member, n, "prefill"), device)
+    rng = np.random.default_rng(37)
+    tokens, top_k = 24, 4
+    x = rng.standard_normal((tokens, 1, 1, n)).astype(np.float16)
+    idx = np.sort(rng.integers(0, EXPERTS, size=(tokens, top_k)), axis=None).reshape(tokens, top_k).astype(np.int32)
+    got = module(torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device), sorted_indices=True)
+    assert tuple(got.shape) == (tokens, top_k, 1, OUT)
+    assert _rel(got, oracle.prefill_reference(ref, x, idx)) < 3e-3
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+def test_prefill_route_serves_unsorted_and_sparse_routing(device, member):
+    """Above the decode limit without sorting: pairs are grouped on the device;
+    only some experts are routed, so compaction leaves slots empty."""
+    n = 2048
+    module, ref = _module(member, n, 43, device)
+    rng = np.random.default_rng(47)
+    tokens, top_k = 40, 2
+    x = rng.standard_normal((tokens, 1, 1, n)).astype(np.float16)
+    idx = rng.choice([1, 6, 3], size=(tokens, top_k)).astype(np.int32)
+    assert idx.size > DECODE_MAT_LIMIT
+    got = module(torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device))
+    assert _rel(got, oracle.prefill_reference(ref, x, idx)) < 3e-3
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+def test_prefill_route_serves_the_sorted_pair_operand(device, member):
+    """x [P, 1, in] with indices [P], the shape a sorting caller hands over."""
+    n = 4096
+    module, ref = _module(member, n, 53, device)
+    rng = np.random.default_rng(61)
+    P = 100
+    x = rng.standard_normal((P, 1, n)).astype(np.float16)
+    idx = np.sort(rng.integers(0, EXPERTS, size=P)).astype(np.int32)
+    got = module(torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device), sorted_indices=True)
+    assert tuple(got.shape) == (P, 1, OUT)
+    assert _rel(got, oracle.prefill_reference(ref, x, idx)) < 3e-3
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+def test_the_two_routes_agree_on_the_same_dispatch(device, member):
+    n = 2048
+    module, _ = _module(member, n, 41, device)
+    rng = np.random.default_rng(43)
+    x = torch.from_numpy(rng.standard_normal((4, 1, 1, n)).astype(np.float16)).to(device)
+    idx = torch.from_numpy(rng.integers(0, EXPERTS, size=(4, 4)).astype(np.int32)).to(device)
+    decode = module.gemv(x, idx).double()
+    prefill = module.prefill(x, idx).double()
+    assert (decode - prefill).abs().max() / prefill.abs().max() < 3e-3
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+def test_gemv_refuses_a_pair_count_that_does_not_tile_the_rows(device, member):
+    module, _ = _module(member, 2048, 61, device)
+    x = torch.zeros((3, 1, 1, 2048), dtype=torch.float16, device=device)
+    idx = torch.zeros((1, 4), dtype=torch.int32, device=device)
+    with pytest.raises(IqkRuntimeError):
+        module.gemv(x, idx)
+
+
+def test_one_layer_can_mix_members(device):
+    rng = np.random.default_rng(47)
+    projections = [
+        ("gate", *_module("iq2_ks", 4096, 51, device), 4096),
+        ("up", *_module("iq2_k", 4096, 53, device), 4096),
+        ("down", *_module("iq1_s_r4", 2048, 57, device, out=512), 2048),
+    ]
+    tokens, top_k = 4, 4
+    idx = rng.integers(0, EXPERTS, size=(tokens, top_k)).astype(np.int32)
+    for name, module, ref, n in projections:
+        x = rng.standard_normal((tokens, 1, 1, n)).astype(np.float16)
+        got = module(torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device))
+        want = np.stack([[ref[idx[t, k]].astype(np.float64) @ x[t, 0, 0].astype(np.float64)
+                          for k in range(top_k)] for t in range(tokens)])[:, :, None, :]
+        assert _rel(got, want) < 1.5e-3, name
+
+
+def test_routed_geometry_at_full_size(device):
+    """256 experts at the gate/up geometry: sampled rows of a top-6 dispatch.
+
+    Full-size parity through a size-independent property: every sampled
+    output row equals its float64 reference, whichever expert it came from.
+    """
+    print("full-size routed geometry", flush=True)
+    member, E, out, n = "iq2_ks", 256, 2048, 4096
+    wire = wirepack.random_wire(member, E * out, n, seed=2024, scales="serving")
+    shapes = fmt.component_shapes(member, E, out, n)
+    module = IqkSwitchLinear(member, E, out, n, device=device)
+    module.load_streams({k: np.ascontiguousarray(v).reshape(shapes[k])
+                         for k, v in fmt.pack(member, wire, n).items()})
+    rng = np.random.default_rng(6)
+    sel = rng.choice(E, 6, replace=False).astype(np.int32)
+    x = rng.standard_normal((1, 1, 1, n)).astype(np.float16)
+    got = module(torch.from_numpy(x).to(device), torch.from_numpy(sel[None]).to(device))
+    got = got.float().cpu().numpy().reshape(6, out).astype(np.float64)
+    rows = rng.choice(out, 64, replace=False)
+    for k, e in enumerate(sel):
+        w = oracle.dequantize(member, wire[e * out + rows], n).astype(np.float64)
+        want = w @ x[0, 0, 0].astype(np.float64)
+        assert np.max(np.abs(got[k, rows] - want)) / np.max(np.abs(want)) < 1.5e-3, e
