@@ -40,9 +40,19 @@ struct Pool {
     uint32_t lo, hi;
 };
 
-__device__ __forceinline__ Pool make_pool(float v0, float v1, float v2, float v3) {
-    const uint32_t p01 = float_to_half_bits(v0) | (float_to_half_bits(v1) << 16);
-    const uint32_t p23 = float_to_half_bits(v2) | (float_to_half_bits(v3) << 16);
+// The four entries are dl * v_c rounded once to fp16.  The products pass
+// through an empty asm so they reach v_cvt_f16_f32 as f32 values: folded into
+// v_fma_mix(dl, v, +0.0) instead, a -0.0 product (a negative scale times a
+// zero index) would come out +0.0, one fp16 bit off the CPU chain.
+__device__ __forceinline__ float opaque(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+__device__ __forceinline__ Pool make_pool(float dl, float v0, float v1, float v2, float v3) {
+    const float y0 = opaque(dl * v0), y1 = opaque(dl * v1), y2 = opaque(dl * v2), y3 = opaque(dl * v3);
+    const uint32_t p01 = float_to_half_bits(y0) | (float_to_half_bits(y1) << 16);
+    const uint32_t p23 = float_to_half_bits(y2) | (float_to_half_bits(y3) << 16);
     return {perm(p23, p01, 0x06040200u), perm(p23, p01, 0x07050301u)};
 }
 
@@ -119,7 +129,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
                 const float dl = d * float(int(idx));
                 const float v0 = alpha ? -26.f : -31.f, v1 = alpha ? -8.f : -13.f;
                 const float v2 = alpha ? 6.f : 1.f, v3 = alpha ? 22.f : 17.f;
-                const Pool p = make_pool(dl * v0, dl * v1, dl * v2, dl * v3);
+                const Pool p = make_pool(dl, v0, v1, v2, v3);
                 expand_word(q[w], p, out + 8 * w);
             }
         }
@@ -141,7 +151,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
                 const float dl = d * float(int(2 * ((h >> 12) & 7u) + 1));
                 const float sh = (h & 0x8000u) ? -0.125f : 0.125f;
                 // grid field f in {0,1,2} decodes to f - 1; field 3 never occurs
-                const Pool p = make_pool(dl * (-1.f + sh), dl * (0.f + sh), dl * (1.f + sh), dl * (2.f + sh));
+                const Pool p = make_pool(dl, -1.f + sh, 0.f + sh, 1.f + sh, 2.f + sh);
                 const uint32_t c0 = grid[(qw & 0xffu) | ((h & 7u) << 8)];
                 const uint32_t c1 = grid[((qw >> 8) & 0xffu) | (((h >> 3) & 7u) << 8)];
                 const uint32_t c2 = grid[((qw >> 16) & 0xffu) | (((h >> 6) & 7u) << 8)];
