@@ -1,0 +1,474 @@
+#!/usr/bin/env python
+"""Routed-expert hot path on one MI355X: decode GEMV, dequant producer, prefill GEMM.
+
+Headline (the JSON line's ``value``): IQ2_KS routed decode of one token over
+256 experts, top-6 -- one step is the gate+up dispatch (12 matrices of
+[2048, 4096] from a 512-expert stack) plus the down dispatch (6 matrices of
+[4096, 2048]) -- as weight-stream bytes per second, the reference's own
+convention (bench/price.py:146).  Inputs are resident in HBM; the K timed
+steps replay as one captured HIP graph between two synchronisations.
+
+Also reported, outside the timed region: every member's decode against its
+own deleted-decode floor (IQ2_KS and IQ1_S_R4 at 1 token, IQ2_K at 8 tokens),
+the dequant producer against its floor, the Zipf(1.1) mixed-member prefill
+(producer GB/s, grouped-GEMM TFLOP/s and MFMA utilisation), and the
+reference's CPU dequantizer + float32 matmul on a bounded sample of the
+headline step.
+
+Protocol (reference: bench/price.py): validation before timing; decode and
+floor arms alternated with the order reversed each round; each arm is a
+captured graph of back-to-back dispatches whose routing variants are disjoint
+chunks of expert permutations, so an expert's bytes are re-read only after
+more than 1 GB of other traffic (beyond the 256 MB MALL).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "mlx-iqk_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+EXPERTS, TOP_K = 256, 6
+GU = (2048, 4096)   # gate/up: out, in
+DN = (4096, 2048)   # down
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200, help="timed headline steps")
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--rounds", type=int, default=3, help="alternated decode/floor rounds per cell")
+    ap.add_argument("--block", type=int, default=100, help="dispatches per captured graph in a cell")
+    ap.add_argument("--distinct", type=int, default=2, help="distinct quantized experts per projection")
+    ap.add_argument("--cells", default="iq2_ks,iq2_k,iq1_s_r4,dequant,prefill")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--json-out", default=None)
+    return ap.parse_args()
+
+
+# --------------------------------------------------------------------- timing ---
+
+
+class Arm:
+    """A captured graph of `count` dispatches; time() replays it once."""
+
+    def __init__(self, torch, launches, label):
+        self.torch, self.label, self.count = torch, label, len(launches)
+        for fn in launches[: min(4, len(launches))]:
+            fn()  # eager warm-up outside capture
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            for fn in launches:
+                fn()
+        torch.cuda.synchronize()
+
+    def time(self) -> float:
+        """Average microseconds per dispatch over one replay (HIP events)."""
+        torch = self.torch
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        self.graph.replay()
+        end.record()
+        end.synchronize()
+        return start.elapsed_time(end) * 1e3 / self.count
+
+
+def alternate(arms: dict, rounds: int) -> dict:
+    names = list(arms)
+    for a in arms.values():
+        a.time()  # one untimed replay each
+    runs = {n: [] for n in names}
+    for r in range(rounds):
+        for n in (names if r % 2 == 0 else names[::-1]):
+            runs[n].append(arms[n].time())
+    return {n: {"median_us": round(statistics.median(v), 3), "min_us": round(min(v), 3),
+                "max_us": round(max(v), 3), "runs_us": [round(x, 3) for x in v]} for n, v in runs.items()}
+
+
+def disjoint_selections(rng, count: int, tokens: int) -> list[np.ndarray]:
+    """`count` routing draws [tokens, TOP_K]; each token's experts are distinct and
+    consecutive draws walk disjoint chunks of fresh permutations."""
+    out, pool = [], []
+    for _ in range(count):
+        sel = np.empty((tokens, TOP_K), dtype=np.int64)
+        for t in range(tokens):
+            if len(pool) < TOP_K:
+                pool = list(rng.permutation(EXPERTS))
+            sel[t] = [pool.pop() for _ in range(TOP_K)]
+        out.append(sel)
+    return out
+
+
+# ---------------------------------------------------------------- decode cells ---
+
+
+def decode_cell(torch, device, member: str, tokens: int, args, seed: int, want_steps: bool = False):
+    from mlx_iqk_amd import format as fmt
+    from mlx_iqk_amd import kernels, synth
+
+    log(f"[decode {member} x{tokens}] building 256-expert stacks")
+    t0 = time.time()
+    gu = synth.expert_stack(member, 2 * EXPERTS, GU[0], GU[1], seed, device, args.distinct, "gate_up")
+    dn = synth.expert_stack(member, EXPERTS, DN[0], DN[1], seed, device, args.distinct, "down")
+    log(f"  stacks ready in {time.time() - t0:.1f}s")
+    rng = np.random.default_rng(seed)
+    variants = 42  # 42 x 6 = 252 experts: one pass over a permutation per 42 dispatches
+    sels = disjoint_selections(rng, variants, tokens)
+    gu_mats, dn_mats = 2 * tokens * TOP_K, tokens * TOP_K
+    V = []
+    for s in sels:
+        flat = s.reshape(-1)
+        V.append({
+            "gu_sel": torch.from_numpy(np.concatenate([flat, flat + EXPERTS]).astype(np.int32)).to(device),
+            "dn_sel": torch.from_numpy(flat.astype(np.int32)).to(device),
+            "gu_x": torch.randn(2 * tokens, GU[1], device=device).to(torch.float16),
+            "dn_x": torch.randn(dn_mats, DN[1], device=device).to(torch.float16),
+            "gu_y": torch.empty(gu_mats, GU[0], dtype=torch.float16, device=device),
+            "dn_y": torch.empty(dn_mats, DN[0], dtype=torch.float16, device=device),
+        })
+
+    def gu_launch(i, floor=False):
+        v = V[i % variants]
+        return lambda: kernels.gemv(member, v["gu_x"], gu, v["gu_sel"], TOP_K, 2 * EXPERTS, GU[0],
+                                    floor=floor, out=v["gu_y"])
+
+    def dn_launch(i, floor=False):
+        v = V[i % variants]
+        return lambda: kernels.gemv(member, v["dn_x"], dn, v["dn_sel"], 1, EXPERTS, DN[0], floor=floor,
+                                    out=v["dn_y"])
+
+    # validation before timing: sampled rows of variant 0 against float64
+    validation = {}
+    for name, launch, stacks, (out, n), mats, ppr in (("gate_up", gu_launch, gu, GU, gu_mats, TOP_K),
+                                                      ("down", dn_launch, dn, DN, dn_mats, 1)):
+        launch(0)()
+        torch.cuda.synchronize()
+        v = V[0]
+        sel = (v["gu_sel"] if name == "gate_up" else v["dn_sel"]).cpu().numpy()
+        x = (v["gu_x"] if name == "gate_up" else v["dn_x"]).cpu().numpy().astype(np.float64)
+        y = (v["gu_y"] if name == "gate_up" else v["dn_y"]).float().cpu().numpy().astype(np.float64)
+        rows = np.random.default_rng(99).choice(out, 32, replace=False)
+        worst = mag = 0.0
+        for m, e in enumerate(sel):
+            part = {k: t[int(e)].cpu().numpy()[rows] for k, t in zip(fmt.component_shapes(member, 1, 1, n), stacks)}
+            w = fmt.decode(member, part, n).astype(np.float64)
+            ref = w @ x[m // ppr]
+            worst = max(worst, float(np.max(np.abs(y[m, rows] - ref))))
+            mag = max(mag, float(np.max(np.abs(ref))))
+        validation[name] = {"rel_dev": worst / mag, "ok": bool(worst / mag < 1.5e-3)}
+        if not validation[name]["ok"]:
+            raise SystemExit(f"{member} {name} failed validation ({worst / mag:.3e}); no timing taken")
+    log(f"  validated: " + ", ".join(f"{k} rel {v['rel_dev']:.2e}" for k, v in validation.items()))
+
+    rb_gu, rb_dn = fmt.ik_row_bytes(member, GU[1]), fmt.ik_row_bytes(member, DN[1])
+    bytes_gu, bytes_dn = gu_mats * GU[0] * rb_gu, dn_mats * DN[0] * rb_dn
+    B = args.block
+    cells = {}
+    for name, launch, nbytes in (("gate_up", gu_launch, bytes_gu), ("down", dn_launch, bytes_dn)):
+        arms = {"decode": Arm(torch, [launch(i) for i in range(B)], "decode"),
+                "floor": Arm(torch, [launch(i, True) for i in range(B)], "floor")}
+        res = alternate(arms, args.rounds)
+        res["bytes_per_dispatch"] = nbytes
+        for arm in ("decode", "floor"):
+            res[arm]["gb_per_s"] = round(nbytes / (res[arm]["median_us"] * 1e-6) / 1e9, 1)
+            res[arm]["frac_of_8tbps"] = round(res[arm]["gb_per_s"] / HBM_PEAK_GBS, 4)
+        res["x_floor"] = round(res["decode"]["median_us"] / res["floor"]["median_us"], 4)
+        res["ideal_us_at_8tbps"] = round(nbytes / HBM_PEAK_GBS / 1e3, 3)
+        cells[name] = res
+        log(f"  {name:8s} decode {res['decode']['median_us']:8.2f} us ({res['decode']['gb_per_s']:7.1f} GB/s)"
+            f"  floor {res['floor']['median_us']:8.2f} us  x{res['x_floor']:.3f}")
+        del arms
+    out = {"member": member, "tokens": tokens, "top_k": TOP_K, "experts": EXPERTS, "validation": validation,
+           "cells": cells}
+    if want_steps:
+        out["_step"] = (gu_launch, dn_launch, bytes_gu + bytes_dn)
+    return out
+
+
+def headline(torch, step, steps: int, warmup: int):
+    """The timed region: K steps (gate/up + down) replayed as one graph."""
+    gu_launch, dn_launch, nbytes = step
+    for i in range(warmup):
+        gu_launch(i)()
+        dn_launch(i)()
+    launches = []
+    for i in range(steps):
+        launches += [gu_launch(i), dn_launch(i)]
+    arm = Arm(torch, launches, "headline")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    us_per_launch = arm.time()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = us_per_launch * 2 / 1e3
+    return {"ms_per_step": ms_per_step, "wall_s": wall, "gb_per_s": nbytes / (ms_per_step * 1e-3) / 1e9,
+            "bytes_per_step": nbytes}
+
+
+# ---------------------------------------------------------------- producer cell ---
+
+
+def dequant_cell(torch, device, member: str, args, seed: int):
+    from mlx_iqk_amd import format as fmt
+    from mlx_iqk_amd import kernels, synth
+
+    res = {}
+    chunk = 16  # experts per dispatch; 16 chunks walk the 256-stack before any re-read
+    for name, (out, n) in (("gate_up", GU), ("down", DN)):
+        log(f"[dequant {member} {name}]")
+        st = synth.expert_stack(member, EXPERTS, out, n, seed, device, args.distinct, f"dq-{name}")
+        w = torch.empty((chunk, out, n), dtype=torch.float16, device=device)
+        parts = [[t[c * chunk:(c + 1) * chunk] for t in st] for c in range(EXPERTS // chunk)]
+        # validation: chunk 0 against the CPU decode, bit for bit (sampled rows)
+        kernels.dequant(member, parts[0], chunk, out, n, out=w)
+        rows = np.random.default_rng(3).choice(out, 8, replace=False)
+        for e in (0, chunk - 1):
+            part = {k: t[e].cpu().numpy()[rows] for k, t in zip(fmt.component_shapes(member, 1, 1, n), parts[0])}
+            want = fmt.decode(member, part, n).astype(np.float16)
+            got = w[e][rows].cpu().numpy()
+            if not np.array_equal(got.view(np.uint16), want.view(np.uint16)):
+                raise SystemExit(f"dequant {member} {name} is not bit-exact; no timing taken")
+        B = max(8, args.block // 8)
+
+        def launch(i, floor=False):
+            return lambda: kernels.dequant(member, parts[i % len(parts)], chunk, out, n, floor=floor, out=w)
+        arms = {"decode": Arm(torch, [launch(i) for i in range(B)], "decode"),
+                "floor": Arm(torch, [launch(i, True) for i in range(B)], "floor")}
+        r = alternate(arms, args.rounds)
+        read = chunk * out * fmt.ik_row_bytes(member, n)
+        written = chunk * out * n * 2
+        r.update({"experts": chunk, "read_bytes": read, "written_bytes": written,
+                  "x_floor": round(r["decode"]["median_us"] / r["floor"]["median_us"], 4)})
+        for arm in ("decode", "floor"):
+            r[arm]["gb_per_s"] = round((read + written) / (r[arm]["median_us"] * 1e-6) / 1e9, 1)
+            r[arm]["frac_of_8tbps"] = round(r[arm]["gb_per_s"] / HBM_PEAK_GBS, 4)
+        res[name] = r
+        log(f"  decode {r['decode']['median_us']:9.2f} us ({r['decode']['gb_per_s']:7.1f} GB/s)  floor "
+            f"{r['floor']['median_us']:9.2f} us  x{r['x_floor']:.3f}")
+        del arms, st, parts, w
+        torch.cuda.empty_cache()
+    return res
+
+
+# ----------------------------------------------------------------- prefill cell ---
+
+
+def prefill_cell(torch, device, args, seed: int):
+    """2048 tokens, Zipf(1.1) top-6 sorted routing; gate/up IQ2_KS, down IQ2_K."""
+    from mlx_iqk_amd import format as fmt
+    from mlx_iqk_amd import kernels, synth
+    from mlx_iqk_amd.nn import IqkSwitchLinear
+
+    tokens = 2048
+    idx = synth.zipf_routing(tokens, EXPERTS, TOP_K, 1.1, seed)
+    flat = np.sort(idx.reshape(-1))
+    counts = np.bincount(flat, minlength=EXPERTS)
+    log(f"[prefill] {flat.size} pairs over {int((counts > 0).sum())} experts, max {counts.max()} "
+        f"median {int(np.median(counts[counts > 0]))} min {counts[counts > 0].min()}")
+    x = torch.randn(flat.size, 1, GU[1], device=device).to(torch.float16)
+    h = torch.randn(flat.size, 1, DN[1], device=device).to(torch.float16)
+    ids = torch.from_numpy(flat.astype(np.int32)).to(device)
+    projections = (("gate", "iq2_ks", GU, x), ("up", "iq2_ks", GU, x), ("down", "iq2_k", DN, h))
+    res = {"tokens": tokens, "pairs": int(flat.size), "experts_routed": int((counts > 0).sum()),
+           "max_pairs_per_expert": int(counts.max()), "projections": {}}
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    tot_prod = tot_gemm = 0.0
+    tot_bytes = tot_flop = 0
+    for name, member, (out, n), xin in projections:
+        mod = IqkSwitchLinear(member, EXPERTS, out, n, device=device)
+        for k, t in zip(mod.stream_names(), synth.expert_stack(member, EXPERTS, out, n, seed, device,
+                                                                 args.distinct, f"pf-{name}")):
+            setattr(mod, k, t)
+        y = mod(xin, ids, sorted_indices=True)  # warm-up + shapes
+        torch.cuda.synchronize()
+        # the two kernels of the route, timed separately with the module's own operands
+        present = torch.zeros(EXPERTS, dtype=torch.int32, device=device).index_fill_(0, ids.long(), 1)
+        slot = torch.where(present > 0, torch.cumsum(present, 0, dtype=torch.int32) - 1,
+                           torch.full_like(present, -1))
+        n_slots = EXPERTS
+        routed = int(present.sum().item())
+        offs = torch.zeros(n_slots + 1, dtype=torch.int32, device=device)
+        offs[1:] = torch.cumsum(torch.zeros(n_slots, dtype=torch.int64, device=device).index_add_(
+            0, slot[ids.long()].long(), torch.ones_like(ids, dtype=torch.int64)), 0).to(torch.int32)
+        rows = torch.arange(flat.size, dtype=torch.int32, device=device)
+        w = torch.empty((n_slots, out, n), dtype=torch.float16, device=device)
+        reps = 3
+        times = {"producer": [], "floor": [], "gemm": []}
+        for _ in range(reps):
+            for key in ("producer", "floor", "gemm"):
+                a, b = ev(), ev()
+                a.record()
+                if key == "gemm":
+                    kernels.grouped_gemm(xin.reshape(-1, n), w, offs, rows)
+                else:
+                    kernels.dequant(member, mod._streams(), EXPERTS, out, n, slot_of_expert=slot, n_slots=n_slots,
+                                    out=w, floor=(key == "floor"))
+                b.record()
+                b.synchronize()
+                times[key].append(a.elapsed_time(b) * 1e3)
+        med = {k: statistics.median(v) for k, v in times.items()}
+        nbytes = routed * out * (fmt.ik_row_bytes(member, n) + 2 * n)
+        flop = 2 * flat.size * out * n
+        r = {"member": member, "experts_reconstructed": routed,
+             "producer_us": round(med["producer"], 2), "producer_floor_us": round(med["floor"], 2),
+             "producer_bytes": nbytes,
+             "producer_gb_per_s": round(nbytes / (med["producer"] * 1e-6) / 1e9, 1),
+             "producer_x_floor": round(med["producer"] / med["floor"], 4),
+             "gemm_us": round(med["gemm"], 2), "gemm_flop": flop,
+             "gemm_tflops": round(flop / (med["gemm"] * 1e-6) / 1e12, 2)}
+        r["mfma_utilisation"] = round(r["gemm_tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
+        res["projections"][name] = r
+        tot_prod += med["producer"]
+        tot_gemm += med["gemm"]
+        tot_bytes += nbytes
+        tot_flop += flop
+        log(f"  {name}: producer {med['producer']:.1f} us ({r['producer_gb_per_s']} GB/s, x{r['producer_x_floor']})"
+            f"  gemm {med['gemm']:.1f} us ({r['gemm_tflops']} TFLOP/s)")
+        del mod, w, y
+        torch.cuda.empty_cache()
+    res["producer_gb_per_s"] = round(tot_bytes / (tot_prod * 1e-6) / 1e9, 1)
+    res["gemm_tflops"] = round(tot_flop / (tot_gemm * 1e-6) / 1e12, 2)
+    res["mfma_utilisation"] = round(res["gemm_tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
+    return res
+
+
+# ------------------------------------------------------------------ CPU baseline ---
+
+
+def cpu_baseline(seconds: float, distinct: int, seed: int) -> dict:
+    """The reference's CPU dequantizer + float32 matmul on the headline step's
+    selected experts (6 x gate, up, down), single-threaded, bounded sample."""
+    from threadpoolctl import threadpool_limits
+
+    from mlx_iqk_amd import format as fmt
+    from mlx_iqk_amd import synth
+    from oracle import oracle
+
+    kind = "reference" if oracle.ref_available() else "port"
+    deq = oracle.ref_dequantize if kind == "reference" else oracle.dequantize
+    member = "iq2_ks"
+    tiles = {}
+    for name, (out, n) in (("gate_up", GU), ("down", DN)):
+        tiles[name] = [synth.quantized_rows(member, out, n, synth.seed_for(seed, name, member, out, n, t),
+                                            imatrix_seed=synth.seed_for(seed, name, "imatrix", n))
+                       for t in range(distinct)]
+    rng = np.random.default_rng(seed)
+    x_gu = rng.standard_normal(GU[1]).astype(np.float16).astype(np.float32)
+    x_dn = rng.standard_normal((TOP_K, DN[1])).astype(np.float16).astype(np.float32)
+    step_bytes = 2 * TOP_K * GU[0] * fmt.ik_row_bytes(member, GU[1]) + TOP_K * DN[0] * fmt.ik_row_bytes(member, DN[1])
+    done, t0 = 0, time.perf_counter()
+    with threadpool_limits(limits=1):
+        while True:
+            sel = rng.choice(EXPERTS, TOP_K, replace=False)
+            for k, e in enumerate(sel):
+                for p in range(2):  # gate, up
+                    wire = tiles["gate_up"][(e + p) % distinct]
+                    w = deq(member, wire, GU[1])
+                    _ = w @ x_gu
+                w = deq(member, tiles["down"][e % distinct], DN[1])
+                _ = w @ x_dn[k]
+            done += 1
+            if time.perf_counter() - t0 >= seconds:
+                break
+    elapsed = time.perf_counter() - t0
+    cpu = platform.processor() or platform.machine()
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(done * step_bytes / elapsed / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"{done} headline steps ({done * 18} matrices: the reference CPU dequantizer on ik wire "
+                      f"+ numpy float32 GEMV, 1 thread) in {elapsed:.1f}s",
+            "ms_per_step": round(elapsed / done * 1e3, 2), "cpu_model": cpu,
+            "host_cpus": len(os.sched_getaffinity(0))}
+
+
+# ------------------------------------------------------------------------- main ---
+
+
+def main() -> int:
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one MI355X: the routed-expert path here runs on a single GPU and has no "
+              f"multi-GPU mode (asked for --gpus {args.gpus}, WORLD_SIZE {world}).", file=sys.stderr)
+        return 2
+    import torch
+
+    device = torch.device("cuda:0")
+    props = torch.cuda.get_device_properties(device)
+    log(f"device {props.name} {props.gcnArchName} CUs {props.multi_processor_count}")
+    cells = [c for c in args.cells.split(",") if c]
+    results = {}
+    t_start = time.time()
+    # the headline member always runs: its gate/up kernel is the roofline kernel
+    results["iq2_ks"] = decode_cell(torch, device, "iq2_ks", 1, args, seed=11, want_steps=True)
+    step = results["iq2_ks"].pop("_step")
+    head = headline(torch, step, args.steps, args.warmup)
+    log(f"[headline] {args.steps} steps: {head['ms_per_step'] * 1e3:.2f} us/step, {head['gb_per_s']:.1f} GB/s")
+    if "iq2_k" in cells:
+        results["iq2_k"] = decode_cell(torch, device, "iq2_k", 8, args, seed=13)
+    if "iq1_s_r4" in cells:
+        results["iq1_s_r4"] = decode_cell(torch, device, "iq1_s_r4", 1, args, seed=17)
+    if "dequant" in cells:
+        results["dequant"] = {m: dequant_cell(torch, device, m, args, seed=19) for m in ("iq2_ks", "iq2_k", "iq1_s_r4")}
+    if "prefill" in cells:
+        results["prefill"] = prefill_cell(torch, device, args, seed=23)
+    base = None if args.no_cpu else cpu_baseline(args.cpu_seconds, args.distinct, seed=11)
+
+    gu = results["iq2_ks"]["cells"]["gate_up"]
+    roofline = {"bound": "hbm", "kernel": "gemv_kernel<IQ2_KS,4096> (gate/up dispatch)",
+                "achieved": gu["decode"]["gb_per_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gu["decode"]["gb_per_s"] / HBM_PEAK_GBS, 4),
+                "per_launch_us": gu["decode"]["median_us"], "bytes_per_launch": gu["bytes_per_dispatch"],
+                "traffic": None}
+    line = {
+        "metric": "routed decode achieved HBM GB/s (IQ2_KS, 256 experts, top-6, 1 token: gate+up and down)",
+        "value": round(head["gb_per_s"], 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(head["ms_per_step"], 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: N(0,0.02) rows, U(0.1,1) imatrix, quantized by the package codec "
+                f"({args.distinct} distinct experts per projection, row-rotated to 256 distinct stacks)",
+        "config": {"workload": "IQ2_KS routed decode, 256 experts, top-6, 1 token, gate/up [2048x4096] x2 "
+                               "+ down [4096x2048]", "experts": EXPERTS, "top_k": TOP_K, "tokens": 1,
+                   "bytes_per_step": head["bytes_per_step"]},
+        "x_floor": {m: {c: r["cells"][c]["x_floor"] for c in r["cells"]} for m, r in results.items()
+                    if "cells" in r},
+        "roofline": roofline,
+        "cpu_baseline": base,
+        "results": results,
+        "elapsed_s": round(time.time() - t_start, 1),
+    }
+    text = json.dumps(line)
+    if args.json_out:
+        Path(args.json_out).write_text(json.dumps(line, indent=2) + "\n")
+    print(text, flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
