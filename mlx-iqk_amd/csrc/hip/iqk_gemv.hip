@@ -294,6 +294,10 @@ int launch_gemv(int64_t n, const GemvArgs &a, uint32_t mats, hipStream_t st) {
     return record_launch(hipGetLastError());
 }
 
+int gemv_mfma_dispatch(bool floor, int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
+                       const void *const *streams, const uint32_t *sel, uint32_t pairs_per_row, uint32_t mats,
+                       void *y, hipStream_t st);
+
 template <bool FLOOR>
 int gemv_entry(int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
                const void *const *streams, int n_streams, const uint32_t *sel, uint32_t pairs_per_row,
@@ -305,6 +309,9 @@ int gemv_entry(int member, int64_t n, int64_t out, int64_t num_experts, const vo
         return IQK_ERR_ARGUMENT;
     if (mats == 0) return IQK_OK;
     if (mats > 65535u) return IQK_ERR_ARGUMENT;
+    hipStream_t st = as_stream(stream);
+    const int r = gemv_mfma_dispatch(FLOOR, member, n, out, num_experts, x, streams, sel, pairs_per_row, mats, y, st);
+    if (r >= 0) return r;
     GemvArgs a;
     a.x = static_cast<const uint32_t *>(x);
     a.s0 = streams[0]; a.s1 = streams[1]; a.s2 = streams[2];
@@ -315,7 +322,6 @@ int gemv_entry(int member, int64_t n, int64_t out, int64_t num_experts, const vo
     a.num_experts = uint32_t(num_experts);
     a.out_features = uint32_t(out);
     a.y = static_cast<uint16_t *>(y);
-    hipStream_t st = as_stream(stream);
     switch (member) {
         case IQK_MEMBER_IQ2_KS: return launch_gemv<IQ2_KS, FLOOR>(n, a, mats, st);
         case IQK_MEMBER_IQ2_K: return launch_gemv<IQ2_K, FLOOR>(n, a, mats, st);

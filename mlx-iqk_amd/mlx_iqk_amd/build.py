@@ -25,7 +25,7 @@ LIBDIR = PACKAGE / "_lib"
 CODEC_LIB = LIBDIR / "libiqk_codec.so"
 HIP_LIB = LIBDIR / "libiqk_hip.so"
 
-HIP_SOURCES = ("iqk_abi.hip", "iqk_gemv.hip", "iqk_dequant.hip", "iqk_gemm.hip")
+HIP_SOURCES = ("iqk_abi.hip", "iqk_gemv.hip", "iqk_gemv_mfma.hip", "iqk_dequant.hip", "iqk_gemm.hip")
 OFFLOAD_ARCH = "gfx950"
 
 

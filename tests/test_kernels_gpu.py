@@ -139,6 +139,57 @@ def test_gemv_matches_a_float64_reference_per_pair_rows(device, member, n):
     _check_gemv(got, oracle.gemv_reference(ref, sel, x, 1), (member, n))
 
 
+@pytest.mark.parametrize("n", kernels.SUPPORTED_IN_FEATURES)
+@pytest.mark.parametrize("out", (16, 48, 192))
+def test_gemv_iq2_ks_tiles(device, n, out):
+    """Row counts on both IQ2_KS paths: 64-row MFMA tiles and 16-row tiles."""
+    print(f"gemv iq2_ks tiles n={n} out={out}", flush=True)
+    experts = 3
+    _, streams, ref = _case("iq2_ks", n, wirepack.seed_for("tiles", n, out), device, experts=experts, out=out)
+    rng = np.random.default_rng(out)
+    x = rng.standard_normal((5, n)).astype(np.float16)
+    sel = rng.integers(0, experts, size=5).astype(np.int32)
+    got = kernels.gemv("iq2_ks", torch.from_numpy(x).to(device), streams, torch.from_numpy(sel).to(device),
+                       1, experts, out).cpu().numpy()
+    _check_gemv(got, oracle.gemv_reference(ref, sel, x, 1), out)
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+@pytest.mark.parametrize("n", kernels.SUPPORTED_IN_FEATURES)
+def test_gemv_activations_of_wide_range(device, member, n):
+    """Activations spanning fp16's range inside one sub-block: subnormals,
+    exact zeros, +-65504 and values 2^-20 below their sub-block's maximum."""
+    print(f"gemv wide-range {member} n={n}", flush=True)
+    _, streams, ref = _case(member, n, wirepack.seed_for(member, n, "wide"), device)
+    rng = np.random.default_rng(29)
+    rows = 6
+    mag = np.exp2(rng.uniform(-24, 6, size=(rows, n)))
+    x = (mag * rng.choice([-1.0, 1.0], size=(rows, n))).astype(np.float16)
+    x[0] = 0
+    x[1, ::7] = 0
+    x[2, 3::1024] = np.float16(65504) * np.where(np.arange(n // 1024) % 2, 1, -1)  # with 2^-24..2^6 neighbours
+    x[3] = np.where(np.arange(n) % 32 == 5, np.float16(1024), np.float16(2.0 ** -10)).astype(np.float16)
+    x[4] = (rng.integers(1, 1023, size=n) * 2.0 ** -24).astype(np.float16)  # subnormals only
+    sel = rng.integers(0, EXPERTS, size=rows).astype(np.int32)
+    with np.errstate(over="ignore"):
+        got = kernels.gemv(member, torch.from_numpy(x).to(device), streams, torch.from_numpy(sel).to(device),
+                           1, EXPERTS, OUT).cpu().numpy()
+    want = oracle.gemv_reference(ref, sel, x, 1)
+    assert np.all(got[0] == 0), member
+    # Row 4's outputs are fp16 subnormals, where the output's own rounding
+    # exceeds 1e-3 relative: it must land within one ULP of the rounded result.
+    assert np.all(_fp16_ulp(got[4], want[4].astype(np.float16)) <= 1), member
+    keep = np.nonzero((np.abs(want).max(axis=1) < 60000) & ~np.isin(np.arange(rows), (0, 4)))[0]
+    assert len(keep) == rows - 2, keep
+    exact = []
+    for r in keep:
+        g, w = got[r].astype(np.float64), want[r]
+        assert np.max(np.abs(g - w)) / np.max(np.abs(w)) < 1.5e-3, (member, n, int(r))
+        assert np.linalg.norm(g - w) / np.linalg.norm(w) <= 1e-3, (member, n, int(r))
+        exact.append(_fp16_ulp(g, w.astype(np.float16)) == 0)
+    assert np.mean(exact) > 0.95, (member, n, np.mean(exact))
+
+
 @pytest.mark.parametrize("member", fmt.MEMBERS)
 def test_gemv_reads_the_expert_the_index_names(device, member):
     n = 2048
