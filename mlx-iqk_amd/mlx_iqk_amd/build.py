@@ -14,6 +14,7 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 from pathlib import Path
 
 PACKAGE = Path(__file__).resolve().parent
@@ -25,7 +26,15 @@ LIBDIR = PACKAGE / "_lib"
 CODEC_LIB = LIBDIR / "libiqk_codec.so"
 HIP_LIB = LIBDIR / "libiqk_hip.so"
 
-HIP_SOURCES = ("iqk_abi.hip", "iqk_gemv.hip", "iqk_gemv_mfma.hip", "iqk_dequant.hip", "iqk_gemm.hip")
+# Source -> extra hipcc flags.  The MFMA decode GEMV folds each accumulator
+# right after its MFMA chain, so its MFMA results go straight to VGPRs.
+HIP_SOURCES = {
+    "iqk_abi.hip": (),
+    "iqk_gemv.hip": (),
+    "iqk_gemv_mfma.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
+    "iqk_dequant.hip": (),
+    "iqk_gemm.hip": (),
+}
 OFFLOAD_ARCH = "gfx950"
 
 
@@ -49,11 +58,15 @@ def codec_command(out: Path = CODEC_LIB) -> list[str]:
             "-o", str(out), str(CSRC / "codec" / "iqk_codec.cpp")]
 
 
-def hip_command(out: Path = HIP_LIB) -> list[str]:
-    return [_hipcc(), f"--offload-arch={OFFLOAD_ARCH}", "-O3", "-fPIC", "-shared", "-std=c++17",
+def hip_object_command(source: str, obj: Path) -> list[str]:
+    return [_hipcc(), f"--offload-arch={OFFLOAD_ARCH}", "-O3", "-fPIC", "-std=c++17",
             # packed fp32 VALU ops stay off: hand the compiler no v_pk_*_f32
             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-            f"-I{INCLUDE}", "-o", str(out)] + [str(CSRC / "hip" / s) for s in HIP_SOURCES]
+            *HIP_SOURCES[source], f"-I{INCLUDE}", "-c", "-o", str(obj), str(CSRC / "hip" / source)]
+
+
+def hip_link_command(objects: list[Path], out: Path) -> list[str]:
+    return [_hipcc(), f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", "-o", str(out)] + [str(o) for o in objects]
 
 
 def build_codec() -> Path:
@@ -65,9 +78,22 @@ def build_codec() -> Path:
 
 
 def build_hip() -> Path:
+    """Compile every source to an object (in parallel, in a temporary
+    directory) and link them into ``libiqk_hip.so``."""
     LIBDIR.mkdir(parents=True, exist_ok=True)
     tmp = HIP_LIB.with_suffix(".so.tmp")
-    _run(hip_command(tmp))
+    with tempfile.TemporaryDirectory(prefix="iqk_hip_") as work:
+        objects = [Path(work) / (Path(s).stem + ".o") for s in HIP_SOURCES]
+        procs = [(cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True))
+                 for cmd in (hip_object_command(s, o) for s, o in zip(HIP_SOURCES, objects))]
+        failures = []
+        for cmd, proc in procs:
+            out, err = proc.communicate()
+            if proc.returncode != 0:
+                failures.append(f"{' '.join(cmd)}\n{out}\n{err}")
+        if failures:
+            raise RuntimeError("build failed: " + "\n".join(failures))
+        _run(hip_link_command(objects, tmp))
     tmp.replace(HIP_LIB)
     return HIP_LIB
 
