@@ -294,9 +294,10 @@ int launch_gemv(int64_t n, const GemvArgs &a, uint32_t mats, hipStream_t st) {
     return record_launch(hipGetLastError());
 }
 
+// The int8-MFMA path (iqk_gemv_mfma.hip); -1 when it does not apply.
 int gemv_mfma_dispatch(bool floor, int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
-                       const void *const *streams, const uint32_t *sel, uint32_t pairs_per_row, uint32_t mats,
-                       void *y, hipStream_t st);
+                       const void *const *streams, int n_streams, const uint32_t *sel, uint32_t pairs_per_row,
+                       uint32_t mats, void *y, hipStream_t st);
 
 template <bool FLOOR>
 int gemv_entry(int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
@@ -310,7 +311,8 @@ int gemv_entry(int member, int64_t n, int64_t out, int64_t num_experts, const vo
     if (mats == 0) return IQK_OK;
     if (mats > 65535u) return IQK_ERR_ARGUMENT;
     hipStream_t st = as_stream(stream);
-    const int r = gemv_mfma_dispatch(FLOOR, member, n, out, num_experts, x, streams, sel, pairs_per_row, mats, y, st);
+    const int r =
+        gemv_mfma_dispatch(FLOOR, member, n, out, num_experts, x, streams, n_streams, sel, pairs_per_row, mats, y, st);
     if (r >= 0) return r;
     GemvArgs a;
     a.x = static_cast<const uint32_t *>(x);

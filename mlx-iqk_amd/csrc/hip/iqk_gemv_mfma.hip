@@ -1,47 +1,62 @@
-// Decode GEMV on int8 MFMA (gfx950), IQ2_KS: the routed decode's fast path.
+// Decode GEMV on int8 MFMA (gfx950) for the three members: the routed
+// decode's fast path.
 //
-// Reference: the Metal decode GEMV (src/mlx_iqk/kernels.py:332-401) computes
-// out[m, r] = half(sum_sb dl_sb * sum_{j in sb} v_j x_j) with an f32 fma chain
-// per lane.  Here the multiply-accumulate runs on v_mfma_i32_16x16x64_i8.
+// Reference: the Metal decode GEMV (src/mlx_iqk/kernels.py:286-401) computes
+// out[m, r] = half(sum_sb dl_sb * sum_{j in sb} w_j x_j) with an f32 fma
+// chain per lane.  Here the multiply-accumulate runs on
+// v_mfma_i32_16x16x64_i8.
 //
-// * Weights.  The two alphabets (-31,-13,1,17) and (-26,-8,6,22) fit int8, so
-//   one v_perm_b32 maps four packed 2-bit codes to four int8 values v, from
-//   a 4-byte pool chosen by the sub-block's alphabet bit.
-// * Activations.  x is converted once per workgroup into an integer with a
-//   per-sub-block power-of-two scale, f = rint(x * 2^E) with |f| <= 2^20,
-//   and split into balanced bytes f = b0 + 2^8 b1 + 2^16 b2 (each b in
-//   [-128, 127]: the bytes of f + 0x808080, each minus 128).  The bytes are
-//   the A operand.  The MFMA's integer sums are exact, so a sub-block's
-//   sum(v x) is exact up to the rounding of x to 2^-20 of its sub-block
-//   maximum (exact for every element within 2^9 of that maximum).  A
-//   sub-block holding an inf or NaN gets a NaN scale, so the rows that read
-//   it come back NaN.
+// * Weights as int8.  IQ2_KS/IQ2_K: both alphabets (-31,-13,1,17) and
+//   (-26,-8,6,22) fit int8.  IQ1_S_R4: 8 * (g + shift) with g in {-1,0,1}
+//   and shift +-1/8 is one of (-7,1,9) or (-9,-1,7).  Either way one
+//   v_perm_b32 maps four packed 2-bit codes to four int8 weights, from a
+//   4-byte pool chosen by the sub-block's alphabet / shift-sign bit.
+//   IQ1_S_R4 looks its eight weights per grid index up in the grid expanded
+//   to int8 (8g + 1) in LDS; the negative shift's 8g - 1 is the exact
+//   correction -2 sum(f) of the block's integer activations.
+// * Activations as integers.  x is converted once per workgroup with a
+//   per-32-element power-of-two scale, f = rint(x * 2^E), |f| <= 2^20, and
+//   split into balanced bytes f = b0 + 2^8 b1 + 2^16 b2 (each b in
+//   [-128, 127]: the bytes of f + 0x808080, each minus 128): the A operand.
+//   The MFMA's integer sums are exact, so each sub-block's sum(w x) is exact
+//   up to the rounding of x to 2^-20 of its 32-element block's maximum
+//   (exact for every element within 2^9 of that maximum).  A block holding
+//   an inf or NaN gets a NaN scale, so the rows that read it come back NaN.
 // * Layout.  A wavefront owns 16 rows (the MFMA's N) and 1024 of the
-//   reduction axis; a workgroup owns 32 rows and all of it, N/1024
-//   wavefronts per 16 rows, so a whole wavefront's compute after its last
-//   byte arrives stays short.  Lane (n, g) = (l%16, l/16).  For super-block
-//   s the four lanes of row n read its 64 contiguous code bytes, lane group g
-//   taking words 16s+4g..16s+4g+3, i.e. sub-blocks 8s+2g and 8s+2g+1.
-//   A-rows 4g..4g+2 carry the byte planes of lane group g's k-range and zero
-//   elsewhere, so D rows 4g..4g+2 -- which the MFMA places in lane group g --
-//   collect exactly that lane's sub-block, one byte plane each.  Two MFMAs
-//   complete a sub-block; each lane then folds one (row, sub-block):
-//   sum(v x) = 2^-E (D0 + 2^8 D1 + 2^16 D2), times the sub-block's index.
-//   Lanes whose A row is zero read a zero span of LDS at the same offsets.
-//   The partial sums of a row's wavefronts meet in LDS.
+//   reduction axis; a workgroup owns 32 rows and all of it (N/1024
+//   wavefronts per 16 rows), so a wavefront's compute after its last byte
+//   arrives stays short.  Lane (n, g) = (l%16, l/16).  In MFMA number m
+//   lane group g holds the 16 weights at k = base(g) + imm(m) of row n:
+//     2-bit members: base = 64g, imm = 256s + 16j (m = 4s + j), so the four
+//       lanes of row n read 64 contiguous code bytes per super-block s;
+//     IQ1_S_R4:      base = 128g, imm = 512i + 16t (m = 8i + t), so they
+//       read 64 contiguous index bytes per i.
+//   A-rows 4g..4g+2 carry the byte planes of lane group g's 16 activations
+//   and zero elsewhere, so D rows 4g..4g+2 -- which the MFMA places in lane
+//   group g -- collect exactly that lane's weights, one byte plane each:
+//   sum(w x) = 2^-E (D0 + 2^8 D1 + 2^16 D2).  Each lane folds its own
+//   (row, sub-block) sums with the sub-block's scale.  Lanes whose A row is
+//   zero read a zero span of LDS at the same offsets.  The partial sums of a
+//   row's wavefronts meet in LDS.
 //
-// The floor variant keeps every global load and deletes the decode.
+// The floor variants keep every global load and delete the decode.
+
+#include <type_traits>
 
 #include "iqk_device.h"
 #include "iqk_host.h"
 
+#define IQK_GRID_STORAGE static constexpr
+#include "../iq1s_grid.h"
+
 namespace iqk {
 
 typedef int int4_t __attribute__((ext_vector_type(4)));
+typedef unsigned short ushort2_t __attribute__((ext_vector_type(2)));
 
 struct Gemv2Args {
     const uint32_t *x;
-    const void *qs, *scl, *sch, *sex, *dv;
+    const void *s0, *s1, *s2, *s3, *s4;
     const uint32_t *sel;
     uint32_t pairs_per_row;
     uint32_t num_experts;
@@ -51,20 +66,21 @@ struct Gemv2Args {
 
 constexpr uint32_t kV8Base = 0x1101F3E1u;   // int8 -31, -13, 1, 17
 constexpr uint32_t kV8Shift = 0x1606F8E6u;  // int8 -26, -8, 6, 22
+constexpr uint32_t kG8Plus = 0x000901F9u;   // int8 8(g + 1/8), g = -1, 0, 1
+constexpr uint32_t kG8Minus = 0x0007FFF7u;  // int8 8(g - 1/8)
 constexpr int kWaveK = 1024;                // reduction elements per wavefront
 constexpr int kGroupRows = 32;              // rows per workgroup
 
 template <int N>
 struct Gemv2Shape {
-    static constexpr int KS = N / kWaveK;     // wavefronts per 16 rows
+    static constexpr int KS = N / kWaveK;  // wavefronts per 16 rows
     static constexpr int THREADS = 64 * 2 * KS;
-    static constexpr int SBW = kWaveK / 256;  // super-blocks per wavefront
     static_assert(N / 8 == THREADS, "one thread per 8 activations");
 };
 
-// The 16 int8 weights of one code word; operand dword s holds codes s, 4+s,
-// 8+s, 12+s (byte t = code 4t+s).
-__device__ __forceinline__ int4_t word_to_v8(uint32_t q, uint32_t pool) {
+// The 16 int8 weights of 16 packed 2-bit codes (code j at bit 2j); operand
+// dword s holds codes s, 4+s, 8+s, 12+s (byte t = code 4t+s).
+__device__ __forceinline__ int4_t codes_to_i8(uint32_t q, uint32_t pool) {
     int4_t b;
     b.x = int(perm(pool, pool, q & 0x03030303u));
     b.y = int(perm(pool, pool, (q >> 2) & 0x03030303u));
@@ -73,9 +89,10 @@ __device__ __forceinline__ int4_t word_to_v8(uint32_t q, uint32_t pool) {
     return b;
 }
 
-// Bit `pos` of w as an all-ones / all-zeros mask.
-__device__ __forceinline__ uint32_t bit_mask(uint32_t w, int pos) {
-    return uint32_t(int32_t(w << (31 - pos)) >> 31);
+// pool_b if bit `pos` of w is set, else pool_a.
+__device__ __forceinline__ uint32_t pick_pool(uint32_t w, int pos, uint32_t pool_a, uint32_t pool_b) {
+    const uint32_t mask = uint32_t(int32_t(w << (31 - pos)) >> 31);
+    return (mask & (pool_a ^ pool_b)) ^ pool_a;
 }
 
 // Plane k, operand dword: bytes k of u[0..3], each minus 128.
@@ -86,27 +103,327 @@ __device__ __forceinline__ void byte_planes(const uint32_t *u, uint32_t &p0, uin
     p2 = (perm(u[1], u[0], 0x0c0c0602u) | perm(u[3], u[2], 0x06020c0cu)) ^ 0x80808080u;
 }
 
-template <int N, bool FLOOR>
-__global__ __launch_bounds__(Gemv2Shape<N>::THREADS) void gemv_mfma_iq2ks(Gemv2Args a) {
+// Byte view of a stream; offsets are 32-bit (the dispatcher checks every
+// stream and the activations fit 4 GiB), so loads take a uniform base and a
+// 32-bit lane offset.
+__device__ __forceinline__ const uint8_t *bytes(const void *p) { return static_cast<const uint8_t *>(p); }
+
+__device__ __forceinline__ int digits_sum(int4_t d) { return d.x + (d.y << 8) + (d.z << 16); }
+
+// IQ1_S_R4's grid expanded to int8 weights 8 * (g + 1/8) = 8g + 1, eight per
+// entry in weight order (two little-endian words), built at compile time from
+// the grid codes (2-bit code c at bit 2k of entry word, g = c - 1).
+struct Iq1B8Table {
+    uint32_t w[2 * IQK_IQ1S_GRID_SIZE];
+};
+
+constexpr Iq1B8Table make_iq1_b8_table() {
+    Iq1B8Table t{};
+    for (int i = 0; i < IQK_IQ1S_GRID_SIZE; ++i)
+        for (int k = 0; k < 8; ++k) {
+            const int c = (iqk_iq1s_grid_codes[i] >> (2 * k)) & 3;
+            const uint32_t b = uint32_t(uint8_t(int8_t(8 * (c - 1) + 1)));
+            t.w[2 * i + k / 4] |= b << (8 * (k % 4));
+        }
+    return t;
+}
+
+__constant__ const Iq1B8Table kIq1B8 = make_iq1_b8_table();
+
+__device__ __forceinline__ int4_t mfma(const uint8_t *a, int4_t b, int4_t c) {
+    const int4_t av = __builtin_bit_cast(int4_t, *reinterpret_cast<const uint4_t *>(a));
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b, c, 0, 0, 0);
+}
+
+// Shared memory of one workgroup: the activations' byte planes [3][N] and a
+// zero span, 2^-E per 32-element block, the wavefronts' partial row sums,
+// and for IQ1_S_R4 the expanded grid and each block's integer sum(f).
+template <int MEMBER, int N>
+struct Gemv2Smem {
+    static constexpr bool IQ1 = MEMBER == IQ1_S_R4;
+    uint8_t dig[3 * N + kWaveK] __attribute__((aligned(16)));
+    float sbs[N / 32];
+    float part[Gemv2Shape<N>::KS][kGroupRows];
+    int fsum[IQ1 ? N / 32 : 1];
+    uint2_t b8[IQ1 ? IQK_IQ1S_GRID_SIZE : 1];
+};
+
+// Activations (fp16) -> balanced byte planes of 16-element words, in the
+// byte order the member's B operand uses.  Thread tid converts 8 activations
+// of word wd, operand dwords 2hp and 2hp+1:
+//   TRANSPOSED (2-bit members): dword s byte t is element 4t+s, so the
+//     thread takes elements 4t+2hp (low halves) and 4t+2hp+1 (high halves)
+//     of the fp16 pairs 2t+hp;
+//   natural (IQ1_S_R4): dword s byte t is element 4s+t, so the thread takes
+//     elements 8hp..8hp+7, the pairs 4hp..4hp+3.
+// With `fsum`, each 32-element block's integer sum(f) lands there too.
+template <int N, bool TRANSPOSED>
+__device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, int *fsum, int tid, uint4_t x0,
+                                                  uint4_t x1) {
+    const uint32_t wd = uint32_t(tid) >> 1, hp = uint32_t(tid) & 1u;
+    if (tid < kWaveK / 16) *reinterpret_cast<uint4_t *>(dig + 3 * N + 16 * tid) = uint4_t{0u, 0u, 0u, 0u};
+    const uint4_t xv = hp ? x1 : x0;
+    const uint32_t xp[4] = {TRANSPOSED ? (hp ? x0.y : x0.x) : xv.x, TRANSPOSED ? (hp ? x0.w : x0.z) : xv.y,
+                            TRANSPOSED ? (hp ? x1.y : x1.x) : xv.z, TRANSPOSED ? (hp ? x1.w : x1.z) : xv.w};
+    // max |x| on the fp16 bits (magnitude order is integer order)
+    ushort2_t m2 = __builtin_bit_cast(ushort2_t, xp[0] & 0x7fff7fffu);
+#pragma unroll
+    for (int t = 1; t < 4; ++t) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(ushort2_t, xp[t] & 0x7fff7fffu));
+    uint32_t mx = max(uint32_t(m2.x), uint32_t(m2.y));
+    mx = max(mx, uint32_t(__shfl_xor(int(mx), 1)));  // the 4 threads of a 32-element block
+    mx = max(mx, uint32_t(__shfl_xor(int(mx), 2)));
+    const bool finite = mx < 0x7c00u;
+    // E so that max|x| * 2^E lies in [2^19, 2^20)
+    const float amax = finite ? half_bits_to_float(mx) : 0.f;
+    const int ex = amax > 0.f ? int((__float_as_uint(amax) >> 23) & 0xffu) - 127 : 0;
+    const int E = 19 - ex;
+    const float up = finite ? __uint_as_float(uint32_t(E + 127) << 23) : 0.f;
+    // x * 2^E + 1.5 * 2^23 rounds x * 2^E to an integer f: the sum stays in
+    // [2^23, 2^24), where the ulp is 1, and its bits are 0x4B400000 + f.
+    // Re-biased, the bits' bytes 0-2 are the bytes of f + 0x808080.
+    constexpr uint32_t kMagicBits = 0x4B400000u;
+    constexpr uint32_t kRebias = 0x808080u - kMagicBits;  // mod 2^32
+    const float magic = __uint_as_float(kMagicBits);
+    uint32_t blo[4], bhi[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        blo[t] = __float_as_uint(fmaf(half_bits_to_float(xp[t] & 0xffffu), up, magic)) + kRebias;
+        bhi[t] = __float_as_uint(fmaf(half_bits_to_float(xp[t] >> 16), up, magic)) + kRebias;
+    }
+    // operand dwords 2hp (u0) and 2hp+1 (u1)
+    uint32_t u0[4], u1[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        if constexpr (TRANSPOSED) {
+            u0[t] = blo[t];
+            u1[t] = bhi[t];
+        } else {
+            const int e = 2 * (t & 1);
+            (t < 2 ? u0 : u1)[e] = blo[t];
+            (t < 2 ? u0 : u1)[e + 1] = bhi[t];
+        }
+    }
+    if (fsum) {  // sum(f) of the block (mod 2^32, exact: |sum| < 2^26)
+        uint32_t f = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) f += blo[t] + bhi[t];
+        f -= 8u * 0x808080u;
+        f += uint32_t(__shfl_xor(int(f), 1));
+        f += uint32_t(__shfl_xor(int(f), 2));
+        if ((tid & 3) == 0) fsum[tid >> 2] = int(f);
+    }
+    uint32_t l0, l1, l2, h0, h1, h2;
+    byte_planes(u0, l0, l1, l2);
+    byte_planes(u1, h0, h1, h2);
+    const uint32_t off = 16 * wd + 8 * hp;
+    *reinterpret_cast<uint2_t *>(dig + 0 * N + off) = uint2_t{l0, h0};
+    *reinterpret_cast<uint2_t *>(dig + 1 * N + off) = uint2_t{l1, h1};
+    *reinterpret_cast<uint2_t *>(dig + 2 * N + off) = uint2_t{l2, h2};
+    if ((tid & 3) == 0) sbs[tid >> 2] = finite ? __uint_as_float(uint32_t(127 - E) << 23) : __builtin_nanf("");
+}
+
+// -- per-member lane state: loads, floor hash, and the decode ---------------------
+
+// IQ2_KS streams: qs u32 [N/16], scl u8 [N/64], sch u8 [N/256], sex u8 [N/256], dv f16.
+template <int N>
+struct LaneIq2ks {
+    uint4_t sc, q[4];
+    uint32_t hb, ab, dvb;
+
+    __device__ __forceinline__ void load(const Gemv2Args &a, uint32_t row, uint32_t kq, uint32_t g) {
+        sc = load_u4(bytes(a.s1) + (row * (N / 64) + 16 * kq));
+        hb = *reinterpret_cast<const uint32_t *>(bytes(a.s2) + (row * (N / 256) + 4 * kq));
+        ab = *reinterpret_cast<const uint32_t *>(bytes(a.s3) + (row * (N / 256) + 4 * kq));
+        dvb = *reinterpret_cast<const uint16_t *>(bytes(a.s4) + 2 * row);
+#pragma unroll
+        for (uint32_t s = 0; s < 4; ++s) q[s] = load_u4(bytes(a.s0) + (row * (N / 4) + 256 * kq + 64 * s + 16 * g));
+    }
+
+    __device__ __forceinline__ uint32_t hash() const {
+        uint32_t h = 59u * (sc.x + sc.y + sc.z + sc.w) + 61u * hb + 71u * ab + 67u * dvb;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) h += q[s].x + 3u * q[s].y + 5u * q[s].z + 7u * q[s].w;
+        return h;
+    }
+
+    // sub-blocks 8s+2g+h (32 weights, words 2h, 2h+1 of q[s])
+    __device__ __forceinline__ float decode(const uint8_t *abase, const float *sbs, int g) const {
+        const uint32_t hbg = hb >> (2 * g), abg = ab >> (2 * g);
+        const uint32_t scg[4] = {sc.x >> (8 * g), sc.y >> (8 * g), sc.z >> (8 * g), sc.w >> (8 * g)};
+        float acc = 0.f;
+        int4_t Dp[2];
+#pragma unroll
+        for (int s = 0; s <= 4; ++s) {
+            int4_t D[2];
+            if (s < 4) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t pool = pick_pool(abg, 8 * s + h, kV8Base, kV8Shift);
+                    D[h] = mfma(abase + 256 * s + 32 * h, codes_to_i8(q[s][2 * h], pool), int4_t{0, 0, 0, 0});
+                    D[h] = mfma(abase + 256 * s + 32 * h + 16, codes_to_i8(q[s][2 * h + 1], pool), D[h]);
+                }
+            }
+            if (s > 0) {  // fold the previous super-block while this one's MFMAs run
+                const int sp = s - 1;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float up = sbs[8 * sp + 2 * g + h];
+                    const int idx = int(((scg[sp] >> (4 * h)) & 15u) | (((hbg >> (8 * sp + h)) & 1u) << 4)) - 16;
+                    acc = fmaf(float(digits_sum(Dp[h])), float(idx) * up, acc);
+                }
+            }
+            if (s < 4) { Dp[0] = D[0]; Dp[1] = D[1]; }
+        }
+        return acc * half_bits_to_float(dvb);
+    }
+};
+
+// IQ2_K streams: qs u32 [N/16], scl u16 [N/64], sex u8 [N/128], dv f16 [N/256].
+template <int N>
+struct LaneIq2k {
+    uint4_t sc0, sc1, q[4];
+    uint2_t ex, dv;
+
+    __device__ __forceinline__ void load(const Gemv2Args &a, uint32_t row, uint32_t kq, uint32_t g) {
+        sc0 = load_u4(bytes(a.s1) + (row * (N / 32) + 32 * kq));
+        sc1 = load_u4(bytes(a.s1) + (row * (N / 32) + 32 * kq + 16));
+        ex = *reinterpret_cast<const uint2_t *>(bytes(a.s2) + (row * (N / 128) + 8 * kq));
+        dv = *reinterpret_cast<const uint2_t *>(bytes(a.s3) + (row * (N / 128) + 8 * kq));
+#pragma unroll
+        for (uint32_t s = 0; s < 4; ++s) q[s] = load_u4(bytes(a.s0) + (row * (N / 4) + 256 * kq + 64 * s + 16 * g));
+    }
+
+    __device__ __forceinline__ uint32_t hash() const {
+        uint32_t h = 59u * (sc0.x + sc0.y + sc0.z + sc0.w + sc1.x + sc1.y + sc1.z + sc1.w) +
+                     71u * (ex.x + ex.y) + 67u * (dv.x + dv.y);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) h += q[s].x + 3u * q[s].y + 5u * q[s].z + 7u * q[s].w;
+        return h;
+    }
+
+    // sub-blocks 16s+4g+j (16 weights, word j of q[s]); d per super-block s
+    __device__ __forceinline__ float decode(const uint8_t *abase, const float *sbs, int g) const {
+        // this lane's scale word of super-block s: u16 4s+g of the wavefront's 16
+        const bool gh = (g >> 1) != 0;
+        const int sh16 = 16 * (g & 1);
+        const uint32_t scw[4] = {(gh ? sc0.y : sc0.x) >> sh16, (gh ? sc0.w : sc0.z) >> sh16,
+                                 (gh ? sc1.y : sc1.x) >> sh16, (gh ? sc1.w : sc1.z) >> sh16};
+        // alphabet bits of super-block s: byte 2s + g/2 of ex, bits 4(g%2) + j
+        const int exs = 8 * (g >> 1) + 4 * (g & 1);
+        const uint32_t exg[2] = {ex.x >> exs, ex.y >> exs};
+        float acc = 0.f;
+        int4_t Dp[4];
+#pragma unroll
+        for (int s = 0; s <= 4; ++s) {
+            int4_t D[4];
+            if (s < 4) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t pool = pick_pool(exg[s >> 1], 16 * (s & 1) + j, kV8Base, kV8Shift);
+                    D[j] = mfma(abase + 256 * s + 16 * j, codes_to_i8(q[s][j], pool), int4_t{0, 0, 0, 0});
+                }
+            }
+            if (s > 0) {
+                const int sp = s - 1;
+                float part = 0.f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float up = sbs[8 * sp + 2 * g + (j >> 1)];
+                    const int idx = int((scw[sp] >> (4 * j)) & 15u) - 8;
+                    part = fmaf(float(digits_sum(Dp[j])), float(idx) * up, part);
+                }
+                acc = fmaf(half_bits_to_float((dv[sp >> 1] >> (16 * (sp & 1))) & 0xffffu), part, acc);
+            }
+            if (s < 4) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) Dp[j] = D[j];
+            }
+        }
+        return acc;
+    }
+};
+
+// IQ1_S_R4 streams: qs u32 [N/32] (4 index bytes per 32-weight block),
+// qh u16 [N/32], dv f16.
+template <int N>
+struct LaneIq1s {
+    uint4_t qv[2];
+    uint2_t qh[2];
+    uint32_t dvb;
+
+    __device__ __forceinline__ void load(const Gemv2Args &a, uint32_t row, uint32_t kq, uint32_t g) {
+        const uint32_t qo = row * (N / 8) + 128 * kq + 16 * g, ho = row * (N / 16) + 64 * kq + 8 * g;
+        qh[0] = *reinterpret_cast<const uint2_t *>(bytes(a.s1) + ho);
+        qh[1] = *reinterpret_cast<const uint2_t *>(bytes(a.s1) + (ho + 32));
+        dvb = *reinterpret_cast<const uint16_t *>(bytes(a.s2) + 2 * row);
+        qv[0] = load_u4(bytes(a.s0) + qo);
+        qv[1] = load_u4(bytes(a.s0) + (qo + 64));
+    }
+
+    __device__ __forceinline__ uint32_t hash() const {
+        return qv[0].x + 3u * qv[0].y + 5u * qv[0].z + 7u * qv[0].w + 11u * qv[1].x + 13u * qv[1].y +
+               17u * qv[1].z + 19u * qv[1].w + 59u * (qh[0].x + qh[0].y) + 61u * (qh[1].x + qh[1].y) + 67u * dvb;
+    }
+
+    // blocks 16i+4g+b (32 weights: index bytes of dword b of qv[i], qh word b
+    // of qh[i]).  The table holds 8g + 1; a block with a negative shift uses
+    // 8g - 1, which takes 2 sum(f) off its digit sum.
+    __device__ __forceinline__ float decode(const uint8_t *abase, const float *sbs, const int *fsum,
+                                            const uint2_t *b8, int g) const {
+        float acc = 0.f;
+        int4_t Dp;
+        uint32_t hp = 0;
+#pragma unroll
+        for (int c = 0; c <= 8; ++c) {  // block c = 4i + b
+            int4_t D;
+            uint32_t hw = 0;
+            if (c < 8) {
+                const int i = c >> 2, b = c & 3;
+                const uint32_t qw = qv[i][b];
+                hw = (qh[i][b >> 1] >> (16 * (b & 1))) & 0xffffu;
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {  // 8-weight groups 2t, 2t+1 of the block
+                    const uint32_t i0 = ((qw >> (16 * t)) & 0xffu) | (((hw >> (6 * t)) & 7u) << 8);
+                    const uint32_t i1 = ((qw >> (16 * t + 8)) & 0xffu) | (((hw >> (6 * t + 3)) & 7u) << 8);
+                    const uint2_t w0 = b8[i0], w1 = b8[i1];
+                    D = mfma(abase + 512 * i + 32 * b + 16 * t, int4_t{int(w0.x), int(w0.y), int(w1.x), int(w1.y)},
+                             t ? D : int4_t{0, 0, 0, 0});
+                }
+            }
+            if (c > 0) {
+                const int cp = c - 1, blk = 16 * (cp >> 2) + 4 * g + (cp & 3);
+                const int neg = int(hp >> 15);
+                const int sint = digits_sum(Dp) - ((2 * fsum[blk]) & -neg);
+                const float ls = float(2 * ((hp >> 12) & 7u) + 1);
+                acc = fmaf(float(sint), ls * sbs[blk], acc);
+            }
+            if (c < 8) { Dp = D; hp = hw; }
+        }
+        return acc * (0.125f * half_bits_to_float(dvb));
+    }
+};
+
+template <int MEMBER, int N>
+using LaneOf = std::conditional_t<MEMBER == IQ2_KS, LaneIq2ks<N>,
+                                  std::conditional_t<MEMBER == IQ2_K, LaneIq2k<N>, LaneIq1s<N>>>;
+
+template <int MEMBER, int N, bool FLOOR>
+__global__ __launch_bounds__(Gemv2Shape<N>::THREADS) void gemv_mfma_kernel(Gemv2Args a) {
     using S = Gemv2Shape<N>;
-    constexpr int KS = S::KS, SBW = S::SBW;
-    // LDS: byte planes [3][N], a zero span [kWaveK], 2^-E per sub-block, partials
-    __shared__ __attribute__((aligned(16))) uint8_t dig[3 * N + kWaveK];
-    __shared__ float sbs[N / 32];
-    __shared__ float part[KS][kGroupRows];
+    constexpr int KS = S::KS;
+    __shared__ Gemv2Smem<MEMBER, N> sm;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, l = tid & 63;
     const int n = l & 15, g = l >> 4;
     const int kq = wave % KS, tile = wave / KS;
-    const uint32_t m = blockIdx.y;
+    const uint32_t tok = blockIdx.z;
+    const uint32_t m = tok * a.pairs_per_row + blockIdx.y;
     const uint32_t rowg = blockIdx.x * kGroupRows;
 
-    // -- activation loads first: they do not wait for the expert id -------------
-    const uint32_t tok = m / a.pairs_per_row;
-    const uint32_t wd = uint32_t(tid) >> 1, hp = uint32_t(tid) & 1u;  // code word of x, half of it
-    const uint32_t *xw = a.x + size_t(tok) * (N / 2) + 8 * wd;
-    const uint4_t x0 = load_u4(xw), x1 = load_u4(xw + 4);
+    // activation loads first: they do not wait for the expert id
+    const uint32_t xo = tok * (2 * N) + 32 * (uint32_t(tid) >> 1);
+    const uint4_t x0 = load_u4(bytes(a.x) + xo), x1 = load_u4(bytes(a.x) + (xo + 16));
 
     const uint32_t e = a.sel[m];
     uint16_t *ygroup = a.y + size_t(m) * a.out_features + rowg;
@@ -114,139 +431,87 @@ __global__ __launch_bounds__(Gemv2Shape<N>::THREADS) void gemv_mfma_iq2ks(Gemv2A
         if (tid < kGroupRows) ygroup[tid] = kHalfNaN;
         return;
     }
-    const size_t row = size_t(e) * a.out_features + rowg + 16 * tile + n;
-
-    // -- this lane's stream bytes: planes first, then the code words -------------
-    const uint4_t scv = load_u4(static_cast<const uint8_t *>(a.scl) + row * (N / 64) + 16 * kq);
-    const uint32_t hbw = *reinterpret_cast<const uint32_t *>(static_cast<const uint8_t *>(a.sch) + row * (N / 256) + 4 * kq);
-    const uint32_t abw = *reinterpret_cast<const uint32_t *>(static_cast<const uint8_t *>(a.sex) + row * (N / 256) + 4 * kq);
-    const uint32_t dvb = static_cast<const uint16_t *>(a.dv)[row];
-    uint4_t q[SBW];
-#pragma unroll
-    for (int s = 0; s < SBW; ++s)
-        q[s] = load_u4(static_cast<const uint32_t *>(a.qs) + row * (N / 16) + 64 * kq + 16 * s + 4 * g);
+    const uint32_t row = e * a.out_features + rowg + 16 * tile + n;
+    LaneOf<MEMBER, N> lane;
+    lane.load(a, row, kq, g);
 
     float acc;
     if constexpr (FLOOR) {
-        uint32_t iacc = x0.x + 3u * x0.y + 5u * x0.z + 7u * x0.w + 11u * x1.x + 13u * x1.y + 17u * x1.z + 19u * x1.w;
-#pragma unroll
-        for (int s = 0; s < SBW; ++s) iacc += q[s].x + 3u * q[s].y + 5u * q[s].z + 7u * q[s].w;
-        iacc += 59u * (scv.x + scv.y + scv.z + scv.w) + 61u * hbw + 71u * abw + 67u * dvb;
-        acc = float(iacc & 0xffu);
+        const uint32_t h = x0.x + 3u * x0.y + 5u * x0.z + 7u * x0.w + 11u * x1.x + 13u * x1.y + 17u * x1.z +
+                           19u * x1.w + lane.hash();
+        acc = float(h & 0xffu);
     } else {
-        // -- activations -> balanced byte planes in LDS ---------------------------
-        if (tid < kWaveK / 16)
-            *reinterpret_cast<uint4_t *>(dig + 3 * N + 16 * tid) = uint4_t{0u, 0u, 0u, 0u};
-        {
-            // This thread's 8 activations: operand dwords 2hp and 2hp+1 of word
-            // wd, i.e. elements 4t + 2hp (low halves) and 4t + 2hp + 1 (high
-            // halves) of the fp16 pairs xp[t] = pair 2t + hp.
-            const uint32_t xp[4] = {hp ? x0.y : x0.x, hp ? x0.w : x0.z, hp ? x1.y : x1.x, hp ? x1.w : x1.z};
-            // max |x| on the fp16 bits (magnitude order is integer order)
-            uint32_t mx = 0;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) mx = max(mx, max(xp[t] & 0x7fffu, (xp[t] >> 16) & 0x7fffu));
-            mx = max(mx, uint32_t(__shfl_xor(int(mx), 1)));  // the 4 threads of a 32-element sub-block
-            mx = max(mx, uint32_t(__shfl_xor(int(mx), 2)));
-            const bool finite = mx < 0x7c00u;
-            // E so that max|x| * 2^E lies in [2^19, 2^20)
-            const float amax = finite ? half_bits_to_float(mx) : 0.f;
-            const int ex = amax > 0.f ? int((__float_as_uint(amax) >> 23) & 0xffu) - 127 : 0;
-            const int E = 19 - ex;
-            const float up = finite ? __uint_as_float(uint32_t(E + 127) << 23) : 0.f;
-            uint32_t ulo[4], uhi[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                ulo[t] = uint32_t(int(__builtin_rintf(half_bits_to_float(xp[t] & 0xffffu) * up)) + 0x808080);
-                uhi[t] = uint32_t(int(__builtin_rintf(half_bits_to_float(xp[t] >> 16) * up)) + 0x808080);
-            }
-            uint32_t l0, l1, l2, h0, h1, h2;
-            byte_planes(ulo, l0, l1, l2);
-            byte_planes(uhi, h0, h1, h2);
-            const uint32_t off = 16 * wd + 8 * hp;
-            *reinterpret_cast<uint2_t *>(dig + 0 * N + off) = uint2_t{l0, h0};
-            *reinterpret_cast<uint2_t *>(dig + 1 * N + off) = uint2_t{l1, h1};
-            *reinterpret_cast<uint2_t *>(dig + 2 * N + off) = uint2_t{l2, h2};
-            if ((tid & 3) == 0)
-                sbs[tid >> 2] = finite ? __uint_as_float(uint32_t(127 - E) << 23) : __builtin_nanf("");
+        constexpr bool IQ1 = MEMBER == IQ1_S_R4;
+        if constexpr (IQ1) {
+            for (int i = tid; i < IQK_IQ1S_GRID_SIZE / 2; i += S::THREADS)
+                reinterpret_cast<uint4_t *>(sm.b8)[i] = reinterpret_cast<const uint4_t *>(kIq1B8.w)[i];
         }
+        stage_activations<N, !IQ1>(sm.dig, sm.sbs, IQ1 ? sm.fsum : nullptr, tid, x0, x1);
         __syncthreads();
-
-        // -- MFMA over the wavefront's 16 rows x 1024 ------------------------------
         const int ai = l & 15;  // this lane's A row
         const bool data = (ai >> 2) == g && (ai & 3) < 3;
-        const uint8_t *abase = dig + (data ? (ai & 3) * N + kWaveK * kq + 64 * g : 3 * N);
-        const uint32_t hbg = hbw >> (2 * g), abg = abw >> (2 * g);
-        const uint32_t scg[4] = {scv.x >> (8 * g), scv.y >> (8 * g), scv.z >> (8 * g), scv.w >> (8 * g)};
-        acc = 0.f;
-        int4_t Dp[2];
-#pragma unroll
-        for (int s = 0; s <= SBW; ++s) {
-            int4_t D[2];
-            if (s < SBW) {
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const uint32_t pool = (bit_mask(abg, 8 * s + h) & (kV8Shift ^ kV8Base)) ^ kV8Base;
-                    D[h] = int4_t{0, 0, 0, 0};
-#pragma unroll
-                    for (int j = 2 * h; j < 2 * h + 2; ++j) {
-                        const int4_t A =
-                            __builtin_bit_cast(int4_t, *reinterpret_cast<const uint4_t *>(abase + 256 * s + 16 * j));
-                        D[h] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, word_to_v8(q[s][j], pool), D[h], 0, 0, 0);
-                    }
-                }
-            }
-            if (s > 0) {  // fold the previous super-block while this one's MFMAs run
-                const int sp = s - 1;
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int sint = Dp[h].x + (Dp[h].y << 8) + (Dp[h].z << 16);
-                    const float up = sbs[8 * (SBW * kq + sp) + 2 * g + h];
-                    const int idx = int(((scg[sp] >> (4 * h)) & 15u) | (((hbg >> (8 * sp + h)) & 1u) << 4)) - 16;
-                    acc = fmaf(float(sint), float(idx) * up, acc);
-                }
-            }
-            if (s < SBW) { Dp[0] = D[0]; Dp[1] = D[1]; }
-        }
-        acc *= half_bits_to_float(dvb);
+        constexpr int LANE_K = IQ1 ? 128 : 64;
+        const uint8_t *abase = sm.dig + (data ? (ai & 3) * N + kWaveK * kq + LANE_K * g : 3 * N);
+        const float *sbs = sm.sbs + (kWaveK / 32) * kq;
+        if constexpr (IQ1)
+            acc = lane.decode(abase, sbs, sm.fsum + (kWaveK / 32) * kq, sm.b8, g);
+        else
+            acc = lane.decode(abase, sbs, g);
     }
     acc += __shfl_xor(acc, 16);
     acc += __shfl_xor(acc, 32);
-    if (g == 0) part[kq][16 * tile + n] = acc;
+    if (g == 0) sm.part[kq][16 * tile + n] = acc;
     __syncthreads();
     if (tid < kGroupRows) {
         float sum = 0.f;
 #pragma unroll
-        for (int k = 0; k < KS; ++k) sum += part[k][tid];
+        for (int k = 0; k < KS; ++k) sum += sm.part[k][tid];
         ygroup[tid] = uint16_t(float_to_half_bits(sum));
     }
 }
 
-template <bool FLOOR>
+template <int MEMBER, bool FLOOR>
 int launch_gemv_mfma(int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t st) {
-    const dim3 grid{a.out_features / kGroupRows, mats};
+    const dim3 grid{a.out_features / kGroupRows, a.pairs_per_row, mats / a.pairs_per_row};
     if (n == 4096)
-        hipLaunchKernelGGL((gemv_mfma_iq2ks<4096, FLOOR>), grid, dim3{Gemv2Shape<4096>::THREADS}, 0, st, a);
+        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 4096, FLOOR>), grid, dim3{Gemv2Shape<4096>::THREADS}, 0, st, a);
     else
-        hipLaunchKernelGGL((gemv_mfma_iq2ks<2048, FLOOR>), grid, dim3{Gemv2Shape<2048>::THREADS}, 0, st, a);
+        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 2048, FLOOR>), grid, dim3{Gemv2Shape<2048>::THREADS}, 0, st, a);
     return record_launch(hipGetLastError());
 }
 
-// Called by the GEMV entry points for IQ2_KS when out_features is a multiple
-// of the workgroup's 32 rows; returns -1 when this path does not apply.
+template <bool FLOOR>
+int launch_member(int member, int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t st) {
+    switch (member) {
+        case IQK_MEMBER_IQ2_KS: return launch_gemv_mfma<IQ2_KS, FLOOR>(n, a, mats, st);
+        case IQK_MEMBER_IQ2_K: return launch_gemv_mfma<IQ2_K, FLOOR>(n, a, mats, st);
+        default: return launch_gemv_mfma<IQ1_S_R4, FLOOR>(n, a, mats, st);
+    }
+}
+
+// Called by the GEMV entry points (after their argument checks) when
+// out_features is a multiple of the workgroup's 32 rows; returns -1 when this
+// path does not apply.
 int gemv_mfma_dispatch(bool floor, int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
-                       const void *const *streams, const uint32_t *sel, uint32_t pairs_per_row, uint32_t mats,
-                       void *y, hipStream_t st) {
-    if (member != IQK_MEMBER_IQ2_KS || out % kGroupRows) return -1;
+                       const void *const *streams, int n_streams, const uint32_t *sel, uint32_t pairs_per_row,
+                       uint32_t mats, void *y, hipStream_t st) {
+    if (out % kGroupRows) return -1;
+    // 32-bit offsets: every stream (the code plane is the largest, N/4 bytes a
+    // row) and the activations stay below 4 GiB
+    const uint64_t lim = uint64_t(1) << 32;
+    if (uint64_t(num_experts) * uint64_t(out) * uint64_t(n / 4) >= lim) return -1;
+    if (uint64_t(mats / pairs_per_row) * uint64_t(2 * n) >= lim) return -1;
     Gemv2Args a;
     a.x = static_cast<const uint32_t *>(x);
-    a.qs = streams[0]; a.scl = streams[1]; a.sch = streams[2]; a.sex = streams[3]; a.dv = streams[4];
+    a.s0 = streams[0]; a.s1 = streams[1]; a.s2 = streams[2];
+    a.s3 = n_streams > 3 ? streams[3] : nullptr;
+    a.s4 = n_streams > 4 ? streams[4] : nullptr;
     a.sel = sel;
     a.pairs_per_row = pairs_per_row;
     a.num_experts = uint32_t(num_experts);
     a.out_features = uint32_t(out);
     a.y = static_cast<uint16_t *>(y);
-    return floor ? launch_gemv_mfma<true>(n, a, mats, st) : launch_gemv_mfma<false>(n, a, mats, st);
+    return floor ? launch_member<true>(member, n, a, mats, st) : launch_member<false>(member, n, a, mats, st);
 }
 
 }  // namespace iqk
