@@ -35,8 +35,9 @@
 //   and zero elsewhere, so D rows 4g..4g+2 -- which the MFMA places in lane
 //   group g -- collect exactly that lane's weights, one byte plane each:
 //   sum(w x) = 2^-E (D0 + 2^8 D1 + 2^16 D2).  Each lane folds its own
-//   (row, sub-block) sums with the sub-block's scale.  Lanes whose A row is
-//   zero read a zero span of LDS at the same offsets.  The partial sums of a
+//   (row, sub-block) sums with the sub-block's scale.  Only the 12 lanes
+//   whose A row carries activations read LDS; the others hold zeros in
+//   registers for the whole kernel.  The partial sums of a
 //   row's wavefronts meet in LDS.
 //
 // The floor variants keep every global load and delete the decode.
@@ -71,11 +72,17 @@ constexpr uint32_t kG8Minus = 0x0007FFF7u;  // int8 8(g - 1/8)
 constexpr int kWaveK = 1024;                // reduction elements per wavefront
 constexpr int kGroupRows = 32;              // rows per workgroup
 
+// Byte planes sit 16 bytes more than N apart, so one lane group's three
+// plane reads fall in different LDS banks.
+template <int N>
+constexpr int kPlaneStride = N + 16;
+
 template <int N>
 struct Gemv2Shape {
     static constexpr int KS = N / kWaveK;  // wavefronts per 16 rows
     static constexpr int THREADS = 64 * 2 * KS;
     static_assert(N / 8 == THREADS, "one thread per 8 activations");
+    static_assert(IQK_IQ1S_GRID_SIZE / 2 % THREADS == 0, "whole uint4 grid chunks per thread");
 };
 
 // The 16 int8 weights of 16 packed 2-bit codes (code j at bit 2j); operand
@@ -130,18 +137,38 @@ constexpr Iq1B8Table make_iq1_b8_table() {
 
 __constant__ const Iq1B8Table kIq1B8 = make_iq1_b8_table();
 
-__device__ __forceinline__ int4_t mfma(const uint8_t *a, int4_t b, int4_t c) {
-    const int4_t av = __builtin_bit_cast(int4_t, *reinterpret_cast<const uint4_t *>(a));
-    return __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b, c, 0, 0, 0);
+__device__ __forceinline__ int4_t mfma(int4_t a, int4_t b, int4_t c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// Shared memory of one workgroup: the activations' byte planes [3][N] and a
-// zero span, 2^-E per 32-element block, the wavefronts' partial row sums,
+// The A operands of K MFMAs, 16 bytes each from p.  Only lanes that carry
+// activations read LDS; the others keep the zeros they start with.
+template <int K>
+__device__ __forceinline__ void read_a(int4_t (&a)[K], const uint8_t *p, bool data) {
+    if (data) {
+#pragma unroll
+        for (int j = 0; j < K; ++j) a[j] = __builtin_bit_cast(int4_t, *reinterpret_cast<const uint4_t *>(p + 16 * j));
+    }
+}
+
+// One A operand read by every lane (non-data lanes point into a zero span).
+__device__ __forceinline__ int4_t read_a_all(const uint8_t *p) {
+    return __builtin_bit_cast(int4_t, *reinterpret_cast<const uint4_t *>(p));
+}
+
+// Whether a member's kernel reads A only in the data lanes (fewer LDS bytes,
+// more live registers) or in every lane from a zero span.  IQ2_K, with a fold
+// per 16 weights, is register-bound and reads in every lane.
+template <int MEMBER>
+constexpr bool kMaskedA = MEMBER != IQ2_K;
+
+// Shared memory of one workgroup: the activations' three byte planes (and a
+// zero span when every lane reads A), 2^-E per 32-element block, the wavefronts' partial row sums,
 // and for IQ1_S_R4 the expanded grid and each block's integer sum(f).
 template <int MEMBER, int N>
 struct Gemv2Smem {
     static constexpr bool IQ1 = MEMBER == IQ1_S_R4;
-    uint8_t dig[3 * N + kWaveK] __attribute__((aligned(16)));
+    uint8_t dig[3 * kPlaneStride<N> + (kMaskedA<MEMBER> ? 0 : kWaveK)] __attribute__((aligned(16)));
     float sbs[N / 32];
     float part[Gemv2Shape<N>::KS][kGroupRows];
     int fsum[IQ1 ? N / 32 : 1];
@@ -156,12 +183,14 @@ struct Gemv2Smem {
 //     of the fp16 pairs 2t+hp;
 //   natural (IQ1_S_R4): dword s byte t is element 4s+t, so the thread takes
 //     elements 8hp..8hp+7, the pairs 4hp..4hp+3.
-// With `fsum`, each 32-element block's integer sum(f) lands there too.
-template <int N, bool TRANSPOSED>
+// With `fsum`, each 32-element block's integer sum(f) lands there too; with
+// ZERO_SPAN, the kWaveK bytes after the planes are cleared.
+template <int N, bool TRANSPOSED, bool ZERO_SPAN>
 __device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, int *fsum, int tid, uint4_t x0,
                                                   uint4_t x1) {
     const uint32_t wd = uint32_t(tid) >> 1, hp = uint32_t(tid) & 1u;
-    if (tid < kWaveK / 16) *reinterpret_cast<uint4_t *>(dig + 3 * N + 16 * tid) = uint4_t{0u, 0u, 0u, 0u};
+    if (ZERO_SPAN && tid < kWaveK / 16)
+        *reinterpret_cast<uint4_t *>(dig + 3 * kPlaneStride<N> + 16 * tid) = uint4_t{0u, 0u, 0u, 0u};
     const uint4_t xv = hp ? x1 : x0;
     const uint32_t xp[4] = {TRANSPOSED ? (hp ? x0.y : x0.x) : xv.x, TRANSPOSED ? (hp ? x0.w : x0.z) : xv.y,
                             TRANSPOSED ? (hp ? x1.y : x1.x) : xv.z, TRANSPOSED ? (hp ? x1.w : x1.z) : xv.w};
@@ -216,9 +245,9 @@ __device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, int 
     byte_planes(u0, l0, l1, l2);
     byte_planes(u1, h0, h1, h2);
     const uint32_t off = 16 * wd + 8 * hp;
-    *reinterpret_cast<uint2_t *>(dig + 0 * N + off) = uint2_t{l0, h0};
-    *reinterpret_cast<uint2_t *>(dig + 1 * N + off) = uint2_t{l1, h1};
-    *reinterpret_cast<uint2_t *>(dig + 2 * N + off) = uint2_t{l2, h2};
+    *reinterpret_cast<uint2_t *>(dig + 0 * kPlaneStride<N> + off) = uint2_t{l0, h0};
+    *reinterpret_cast<uint2_t *>(dig + 1 * kPlaneStride<N> + off) = uint2_t{l1, h1};
+    *reinterpret_cast<uint2_t *>(dig + 2 * kPlaneStride<N> + off) = uint2_t{l2, h2};
     if ((tid & 3) == 0) sbs[tid >> 2] = finite ? __uint_as_float(uint32_t(127 - E) << 23) : __builtin_nanf("");
 }
 
@@ -247,20 +276,21 @@ struct LaneIq2ks {
     }
 
     // sub-blocks 8s+2g+h (32 weights, words 2h, 2h+1 of q[s])
-    __device__ __forceinline__ float decode(const uint8_t *abase, const float *sbs, int g) const {
+    __device__ __forceinline__ float decode(const uint8_t *abase, bool data, const float *sbs, int g) const {
         const uint32_t hbg = hb >> (2 * g), abg = ab >> (2 * g);
         const uint32_t scg[4] = {sc.x >> (8 * g), sc.y >> (8 * g), sc.z >> (8 * g), sc.w >> (8 * g)};
         float acc = 0.f;
-        int4_t Dp[2];
+        int4_t Dp[2], A[4] = {};
 #pragma unroll
         for (int s = 0; s <= 4; ++s) {
             int4_t D[2];
             if (s < 4) {
+                read_a(A, abase + 256 * s, data);
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const uint32_t pool = pick_pool(abg, 8 * s + h, kV8Base, kV8Shift);
-                    D[h] = mfma(abase + 256 * s + 32 * h, codes_to_i8(q[s][2 * h], pool), int4_t{0, 0, 0, 0});
-                    D[h] = mfma(abase + 256 * s + 32 * h + 16, codes_to_i8(q[s][2 * h + 1], pool), D[h]);
+                    D[h] = mfma(A[2 * h], codes_to_i8(q[s][2 * h], pool), int4_t{0, 0, 0, 0});
+                    D[h] = mfma(A[2 * h + 1], codes_to_i8(q[s][2 * h + 1], pool), D[h]);
                 }
             }
             if (s > 0) {  // fold the previous super-block while this one's MFMAs run
@@ -311,33 +341,27 @@ struct LaneIq2k {
         // alphabet bits of super-block s: byte 2s + g/2 of ex, bits 4(g%2) + j
         const int exs = 8 * (g >> 1) + 4 * (g & 1);
         const uint32_t exg[2] = {ex.x >> exs, ex.y >> exs};
-        float acc = 0.f;
-        int4_t Dp[4];
+        float acc = 0.f, part = 0.f;
+        int4_t Dp;
 #pragma unroll
-        for (int s = 0; s <= 4; ++s) {
-            int4_t D[4];
-            if (s < 4) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t pool = pick_pool(exg[s >> 1], 16 * (s & 1) + j, kV8Base, kV8Shift);
-                    D[j] = mfma(abase + 256 * s + 16 * j, codes_to_i8(q[s][j], pool), int4_t{0, 0, 0, 0});
+        for (int w = 0; w <= 16; ++w) {  // word w = 4s + j; fold word w-1 while w's MFMA runs
+            int4_t D;
+            if (w < 16) {
+                const int s = w >> 2, j = w & 3;
+                const uint32_t pool = pick_pool(exg[s >> 1], 16 * (s & 1) + j, kV8Base, kV8Shift);
+                D = mfma(read_a_all(abase + 256 * s + 16 * j), codes_to_i8(q[s][j], pool), int4_t{0, 0, 0, 0});
+            }
+            if (w > 0) {
+                const int s = (w - 1) >> 2, j = (w - 1) & 3;
+                const float up = sbs[8 * s + 2 * g + (j >> 1)];
+                const int idx = int((scw[s] >> (4 * j)) & 15u) - 8;
+                part = fmaf(float(digits_sum(Dp)), float(idx) * up, part);
+                if (j == 3) {
+                    acc = fmaf(half_bits_to_float((dv[s >> 1] >> (16 * (s & 1))) & 0xffffu), part, acc);
+                    part = 0.f;
                 }
             }
-            if (s > 0) {
-                const int sp = s - 1;
-                float part = 0.f;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float up = sbs[8 * sp + 2 * g + (j >> 1)];
-                    const int idx = int((scw[sp] >> (4 * j)) & 15u) - 8;
-                    part = fmaf(float(digits_sum(Dp[j])), float(idx) * up, part);
-                }
-                acc = fmaf(half_bits_to_float((dv[sp >> 1] >> (16 * (sp & 1))) & 0xffffu), part, acc);
-            }
-            if (s < 4) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) Dp[j] = D[j];
-            }
+            if (w < 16) Dp = D;
         }
         return acc;
     }
@@ -368,10 +392,10 @@ struct LaneIq1s {
     // blocks 16i+4g+b (32 weights: index bytes of dword b of qv[i], qh word b
     // of qh[i]).  The table holds 8g + 1; a block with a negative shift uses
     // 8g - 1, which takes 2 sum(f) off its digit sum.
-    __device__ __forceinline__ float decode(const uint8_t *abase, const float *sbs, const int *fsum,
+    __device__ __forceinline__ float decode(const uint8_t *abase, bool data, const float *sbs, const int *fsum,
                                             const uint2_t *b8, int g) const {
         float acc = 0.f;
-        int4_t Dp;
+        int4_t Dp, A[4] = {};
         uint32_t hp = 0;
 #pragma unroll
         for (int c = 0; c <= 8; ++c) {  // block c = 4i + b
@@ -379,6 +403,7 @@ struct LaneIq1s {
             uint32_t hw = 0;
             if (c < 8) {
                 const int i = c >> 2, b = c & 3;
+                if ((b & 1) == 0) read_a(A, abase + 512 * i + 32 * b, data);  // blocks b, b+1
                 const uint32_t qw = qv[i][b];
                 hw = (qh[i][b >> 1] >> (16 * (b & 1))) & 0xffffu;
 #pragma unroll
@@ -386,7 +411,7 @@ struct LaneIq1s {
                     const uint32_t i0 = ((qw >> (16 * t)) & 0xffu) | (((hw >> (6 * t)) & 7u) << 8);
                     const uint32_t i1 = ((qw >> (16 * t + 8)) & 0xffu) | (((hw >> (6 * t + 3)) & 7u) << 8);
                     const uint2_t w0 = b8[i0], w1 = b8[i1];
-                    D = mfma(abase + 512 * i + 32 * b + 16 * t, int4_t{int(w0.x), int(w0.y), int(w1.x), int(w1.y)},
+                    D = mfma(A[2 * (b & 1) + t], int4_t{int(w0.x), int(w0.y), int(w1.x), int(w1.y)},
                              t ? D : int4_t{0, 0, 0, 0});
                 }
             }
@@ -407,8 +432,12 @@ template <int MEMBER, int N>
 using LaneOf = std::conditional_t<MEMBER == IQ2_KS, LaneIq2ks<N>,
                                   std::conditional_t<MEMBER == IQ2_K, LaneIq2k<N>, LaneIq1s<N>>>;
 
+// Six wavefronts per SIMD: three workgroups of eight (N = 4096) or six of
+// four (N = 2048) per CU, so a 1-token routed decode's 768 workgroups are
+// resident at once.
 template <int MEMBER, int N, bool FLOOR>
-__global__ __launch_bounds__(Gemv2Shape<N>::THREADS) void gemv_mfma_kernel(Gemv2Args a) {
+__global__ __launch_bounds__(Gemv2Shape<N>::THREADS) __attribute__((amdgpu_waves_per_eu(6)))
+void gemv_mfma_kernel(Gemv2Args a) {
     using S = Gemv2Shape<N>;
     constexpr int KS = S::KS;
     __shared__ Gemv2Smem<MEMBER, N> sm;
@@ -421,9 +450,17 @@ __global__ __launch_bounds__(Gemv2Shape<N>::THREADS) void gemv_mfma_kernel(Gemv2
     const uint32_t m = tok * a.pairs_per_row + blockIdx.y;
     const uint32_t rowg = blockIdx.x * kGroupRows;
 
-    // activation loads first: they do not wait for the expert id
+    // Activation (and IQ1_S_R4 grid) loads first: they do not wait for the
+    // expert id, and vector loads retire in order, so staging them waits for
+    // none of the stream bytes issued after them.
     const uint32_t xo = tok * (2 * N) + 32 * (uint32_t(tid) >> 1);
     const uint4_t x0 = load_u4(bytes(a.x) + xo), x1 = load_u4(bytes(a.x) + (xo + 16));
+    constexpr bool IQ1 = MEMBER == IQ1_S_R4;
+    constexpr int GRID_CHUNKS = IQ1 && !FLOOR ? IQK_IQ1S_GRID_SIZE / 2 / S::THREADS : 0;  // uint4 per thread
+    uint4_t gridv[GRID_CHUNKS > 0 ? GRID_CHUNKS : 1];
+#pragma unroll
+    for (int i = 0; i < GRID_CHUNKS; ++i)
+        gridv[i] = reinterpret_cast<const uint4_t *>(kIq1B8.w)[tid + i * S::THREADS];
 
     const uint32_t e = a.sel[m];
     uint16_t *ygroup = a.y + size_t(m) * a.out_features + rowg;
@@ -441,20 +478,20 @@ __global__ __launch_bounds__(Gemv2Shape<N>::THREADS) void gemv_mfma_kernel(Gemv2
                            19u * x1.w + lane.hash();
         acc = float(h & 0xffu);
     } else {
-        constexpr bool IQ1 = MEMBER == IQ1_S_R4;
-        if constexpr (IQ1) {
-            for (int i = tid; i < IQK_IQ1S_GRID_SIZE / 2; i += S::THREADS)
-                reinterpret_cast<uint4_t *>(sm.b8)[i] = reinterpret_cast<const uint4_t *>(kIq1B8.w)[i];
-        }
-        stage_activations<N, !IQ1>(sm.dig, sm.sbs, IQ1 ? sm.fsum : nullptr, tid, x0, x1);
+#pragma unroll
+        for (int i = 0; i < GRID_CHUNKS; ++i) reinterpret_cast<uint4_t *>(sm.b8)[tid + i * S::THREADS] = gridv[i];
+        stage_activations<N, !IQ1, !kMaskedA<MEMBER>>(sm.dig, sm.sbs, IQ1 ? sm.fsum : nullptr, tid, x0, x1);
         __syncthreads();
         const int ai = l & 15;  // this lane's A row
         const bool data = (ai >> 2) == g && (ai & 3) < 3;
         constexpr int LANE_K = IQ1 ? 128 : 64;
-        const uint8_t *abase = sm.dig + (data ? (ai & 3) * N + kWaveK * kq + LANE_K * g : 3 * N);
+        const uint8_t *abase = sm.dig + (data || kMaskedA<MEMBER> ? (ai & 3) * kPlaneStride<N> + kWaveK * kq + LANE_K * g
+                                                                 : 3 * kPlaneStride<N>);
         const float *sbs = sm.sbs + (kWaveK / 32) * kq;
         if constexpr (IQ1)
-            acc = lane.decode(abase, sbs, sm.fsum + (kWaveK / 32) * kq, sm.b8, g);
+            acc = lane.decode(abase, data, sbs, sm.fsum + (kWaveK / 32) * kq, sm.b8, g);
+        else if constexpr (MEMBER == IQ2_KS)
+            acc = lane.decode(abase, data, sbs, g);
         else
             acc = lane.decode(abase, sbs, g);
     }
