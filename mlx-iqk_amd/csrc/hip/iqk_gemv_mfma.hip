@@ -37,8 +37,8 @@
 //   sum(w x) = 2^-E (D0 + 2^8 D1 + 2^16 D2).  Each lane folds its own
 //   (row, sub-block) sums with the sub-block's scale.  Only the 12 lanes
 //   whose A row carries activations read LDS; the others hold zeros in
-//   registers for the whole kernel.  The partial sums of a
-//   row's wavefronts meet in LDS.
+//   registers for the whole kernel.  The partial sums of a row's lanes and
+//   wavefronts meet in LDS.
 //
 // The floor variants keep every global load and delete the decode.
 
@@ -115,6 +115,13 @@ __device__ __forceinline__ void byte_planes(const uint32_t *u, uint32_t &p0, uin
 // 32-bit lane offset.
 __device__ __forceinline__ const uint8_t *bytes(const void *p) { return static_cast<const uint8_t *>(p); }
 
+// The value of lane (l ^ X) within l's quad (X = 1, 2), by a DPP quad permute.
+template <int X>
+__device__ __forceinline__ uint32_t quad_xor(uint32_t v) {
+    constexpr int ctrl = X == 1 ? 0xB1 : 0x4E;  // quad_perm [1,0,3,2] / [2,3,0,1]
+    return uint32_t(__builtin_amdgcn_mov_dpp(int(v), ctrl, 0xF, 0xF, false));
+}
+
 __device__ __forceinline__ int digits_sum(int4_t d) { return d.x + (d.y << 8) + (d.z << 16); }
 
 // IQ1_S_R4's grid expanded to int8 weights 8 * (g + 1/8) = 8g + 1, eight per
@@ -170,7 +177,7 @@ struct Gemv2Smem {
     static constexpr bool IQ1 = MEMBER == IQ1_S_R4;
     uint8_t dig[3 * kPlaneStride<N> + (kMaskedA<MEMBER> ? 0 : kWaveK)] __attribute__((aligned(16)));
     float sbs[N / 32];
-    float part[Gemv2Shape<N>::KS][kGroupRows];
+    float part[Gemv2Shape<N>::KS][4][kGroupRows];
     int fsum[IQ1 ? N / 32 : 1];
     uint2_t b8[IQ1 ? IQK_IQ1S_GRID_SIZE : 1];
 };
@@ -199,8 +206,8 @@ __device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, int 
 #pragma unroll
     for (int t = 1; t < 4; ++t) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(ushort2_t, xp[t] & 0x7fff7fffu));
     uint32_t mx = max(uint32_t(m2.x), uint32_t(m2.y));
-    mx = max(mx, uint32_t(__shfl_xor(int(mx), 1)));  // the 4 threads of a 32-element block
-    mx = max(mx, uint32_t(__shfl_xor(int(mx), 2)));
+    mx = max(mx, quad_xor<1>(mx));  // the 4 threads of a 32-element block
+    mx = max(mx, quad_xor<2>(mx));
     const bool finite = mx < 0x7c00u;
     // E so that max|x| * 2^E lies in [2^19, 2^20)
     const float amax = finite ? half_bits_to_float(mx) : 0.f;
@@ -237,8 +244,8 @@ __device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, int 
 #pragma unroll
         for (int t = 0; t < 4; ++t) f += blo[t] + bhi[t];
         f -= 8u * 0x808080u;
-        f += uint32_t(__shfl_xor(int(f), 1));
-        f += uint32_t(__shfl_xor(int(f), 2));
+        f += quad_xor<1>(f);
+        f += quad_xor<2>(f);
         if ((tid & 3) == 0) fsum[tid >> 2] = int(f);
     }
     uint32_t l0, l1, l2, h0, h1, h2;
@@ -495,14 +502,12 @@ void gemv_mfma_kernel(Gemv2Args a) {
         else
             acc = lane.decode(abase, sbs, g);
     }
-    acc += __shfl_xor(acc, 16);
-    acc += __shfl_xor(acc, 32);
-    if (g == 0) sm.part[kq][16 * tile + n] = acc;
+    sm.part[kq][g][16 * tile + n] = acc;
     __syncthreads();
     if (tid < kGroupRows) {
         float sum = 0.f;
 #pragma unroll
-        for (int k = 0; k < KS; ++k) sum += sm.part[k][tid];
+        for (int k = 0; k < KS; ++k) sum += (sm.part[k][0][tid] + sm.part[k][1][tid]) + (sm.part[k][2][tid] + sm.part[k][3][tid]);
         ygroup[tid] = uint16_t(float_to_half_bits(sum));
     }
 }
