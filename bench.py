@@ -43,6 +43,7 @@ for _p in (ROOT / "mlx-iqk_amd", ROOT):
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 EXPERTS, TOP_K = 256, 6
+PROBE_COPY_BYTES = 64 << 20
 GU = (2048, 4096)   # gate/up: out, in
 DN = (4096, 2048)   # down
 
@@ -56,13 +57,17 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200, help="timed headline steps")
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--rounds", type=int, default=3, help="alternated decode/floor rounds per cell")
-    ap.add_argument("--block", type=int, default=100, help="dispatches per captured graph in a cell")
+    ap.add_argument("--rounds", type=int, default=5, help="alternated decode/floor rounds per cell")
+    ap.add_argument("--block", type=int, default=200, help="dispatches per captured graph in a cell")
     ap.add_argument("--distinct", type=int, default=2, help="distinct quantized experts per projection")
     ap.add_argument("--cells", default="iq2_ks,iq2_k,iq1_s_r4,dequant,prefill")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0,
+                    help="CPU baseline sample budget (half on one thread, half on every core)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--json-out", default=None)
+    ap.add_argument("--probe", type=int, default=0, metavar="K",
+                    help="counter-probe mode: K eager IQ2_KS gate/up decode dispatches, then K copies of "
+                         f"{PROBE_COPY_BYTES >> 20} MiB (the HBM-byte calibration), and exit")
     return ap.parse_args()
 
 
@@ -123,7 +128,8 @@ def disjoint_selections(rng, count: int, tokens: int) -> list[np.ndarray]:
 # ---------------------------------------------------------------- decode cells ---
 
 
-def decode_cell(torch, device, member: str, tokens: int, args, seed: int, want_steps: bool = False):
+def decode_cell(torch, device, member: str, tokens: int, args, seed: int, want_steps: bool = False,
+                launchers_only: bool = False):
     from mlx_iqk_amd import format as fmt
     from mlx_iqk_amd import kernels, synth
 
@@ -180,6 +186,8 @@ def decode_cell(torch, device, member: str, tokens: int, args, seed: int, want_s
         if not validation[name]["ok"]:
             raise SystemExit(f"{member} {name} failed validation ({worst / mag:.3e}); no timing taken")
     log(f"  validated: " + ", ".join(f"{k} rel {v['rel_dev']:.2e}" for k, v in validation.items()))
+    if launchers_only:
+        return gu_launch, dn_launch
 
     rb_gu, rb_dn = fmt.ik_row_bytes(member, GU[1]), fmt.ik_row_bytes(member, DN[1])
     bytes_gu, bytes_dn = gu_mats * GU[0] * rb_gu, dn_mats * DN[0] * rb_dn
@@ -356,9 +364,25 @@ def prefill_cell(torch, device, args, seed: int):
 # ------------------------------------------------------------------ CPU baseline ---
 
 
+def _cpu_model() -> str:
+    cpu = platform.processor() or platform.machine()
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return cpu
+
+
 def cpu_baseline(seconds: float, distinct: int, seed: int) -> dict:
     """The reference's CPU dequantizer + float32 matmul on the headline step's
-    selected experts (6 x gate, up, down), single-threaded, bounded sample."""
+    selected experts (6 x gate, up, down), on a bounded sample: once on one
+    thread, once on every host core (one matrix per worker; the compiled
+    dequantizer releases the GIL, numpy's BLAS is held to one thread per
+    worker).  The all-core run is the reported value."""
+    from concurrent.futures import ThreadPoolExecutor
+
     from threadpoolctl import threadpool_limits
 
     from mlx_iqk_amd import format as fmt
@@ -377,34 +401,62 @@ def cpu_baseline(seconds: float, distinct: int, seed: int) -> dict:
     x_gu = rng.standard_normal(GU[1]).astype(np.float16).astype(np.float32)
     x_dn = rng.standard_normal((TOP_K, DN[1])).astype(np.float16).astype(np.float32)
     step_bytes = 2 * TOP_K * GU[0] * fmt.ik_row_bytes(member, GU[1]) + TOP_K * DN[0] * fmt.ik_row_bytes(member, DN[1])
-    done, t0 = 0, time.perf_counter()
-    with threadpool_limits(limits=1):
-        while True:
-            sel = rng.choice(EXPERTS, TOP_K, replace=False)
-            for k, e in enumerate(sel):
-                for p in range(2):  # gate, up
-                    wire = tiles["gate_up"][(e + p) % distinct]
-                    w = deq(member, wire, GU[1])
-                    _ = w @ x_gu
-                w = deq(member, tiles["down"][e % distinct], DN[1])
-                _ = w @ x_dn[k]
-            done += 1
-            if time.perf_counter() - t0 >= seconds:
-                break
-    elapsed = time.perf_counter() - t0
-    cpu = platform.processor() or platform.machine()
-    try:
-        for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": round(done * step_bytes / elapsed / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": f"{done} headline steps ({done * 18} matrices: the reference CPU dequantizer on ik wire "
-                      f"+ numpy float32 GEMV, 1 thread) in {elapsed:.1f}s",
-            "ms_per_step": round(elapsed / done * 1e3, 2), "cpu_model": cpu,
-            "host_cpus": len(os.sched_getaffinity(0))}
+
+    def matrix(job):
+        wire, n, x = job
+        return deq(member, wire, n) @ x
+
+    def step_jobs():
+        sel = rng.choice(EXPERTS, TOP_K, replace=False)
+        jobs = []
+        for k, e in enumerate(sel):
+            for p in range(2):  # gate, up
+                jobs.append((tiles["gate_up"][(e + p) % distinct], GU[1], x_gu))
+            jobs.append((tiles["down"][e % distinct], DN[1], x_dn[k]))
+        return jobs
+
+    def run(threads: int, budget: float) -> dict:
+        done, t0 = 0, time.perf_counter()
+        with threadpool_limits(limits=1), ThreadPoolExecutor(max_workers=threads) as pool:
+            while True:
+                list(pool.map(matrix, step_jobs()))
+                done += 1
+                if time.perf_counter() - t0 >= budget:
+                    break
+        elapsed = time.perf_counter() - t0
+        return {"value": round(done * step_bytes / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads,
+                "steps": done, "seconds": round(elapsed, 2), "ms_per_step": round(elapsed / done * 1e3, 2)}
+
+    cores = len(os.sched_getaffinity(0))
+    matrix(step_jobs()[0])  # untimed: loads the dequantizer library before any worker starts
+    one = run(1, seconds / 2)
+    every = run(cores, seconds / 2)
+    return {"value": every["value"], "unit": "GB/s", "cores": cores, "kind": kind,
+            "sample": f"{every['steps']} headline steps ({every['steps'] * 18} matrices: the reference CPU "
+                      f"dequantizer on ik wire + numpy float32 GEMV, one matrix per worker on {cores} threads) "
+                      f"in {every['seconds']}s",
+            "ms_per_step": every["ms_per_step"], "single_thread": one, "cpu_model": _cpu_model(),
+            "host_cpus": cores}
+
+
+def probe(torch, device, args) -> int:
+    """Eager dispatches for hardware-counter passes (rocprofv3 --pmc): the
+    headline gate/up decode kernel on its disjoint routing variants, then a
+    plain device copy of known size whose counters calibrate HBM bytes."""
+    from mlx_iqk_amd.format import ik_row_bytes
+
+    gu_launch, _ = decode_cell(torch, device, "iq2_ks", 1, args, seed=11, launchers_only=True)
+    for i in range(args.probe):
+        gu_launch(i)()
+    src = torch.empty(PROBE_COPY_BYTES, dtype=torch.uint8, device=device).random_(0, 255)
+    dst = torch.empty_like(src)
+    for _ in range(args.probe):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": args.probe, "kernel": "gemv_mfma_kernel<IQ2_KS,4096>",
+                      "bytes_per_dispatch": 2 * TOP_K * GU[0] * ik_row_bytes("iq2_ks", GU[1]),
+                      "copy_bytes": PROBE_COPY_BYTES}), flush=True)
+    return 0
 
 
 # ------------------------------------------------------------------------- main ---
@@ -422,6 +474,8 @@ def main() -> int:
     device = torch.device("cuda:0")
     props = torch.cuda.get_device_properties(device)
     log(f"device {props.name} {props.gcnArchName} CUs {props.multi_processor_count}")
+    if args.probe:
+        return probe(torch, device, args)
     cells = [c for c in args.cells.split(",") if c]
     results = {}
     t_start = time.time()
@@ -441,16 +495,20 @@ def main() -> int:
     base = None if args.no_cpu else cpu_baseline(args.cpu_seconds, args.distinct, seed=11)
 
     gu = results["iq2_ks"]["cells"]["gate_up"]
-    roofline = {"bound": "hbm", "kernel": "gemv_kernel<IQ2_KS,4096> (gate/up dispatch)",
+    traffic_file = ROOT / "profiles" / "gemv_mfma_iq2_ks_gate_up_traffic.json"
+    traffic = json.loads(traffic_file.read_text())["traffic_bytes"] if traffic_file.is_file() else None
+    roofline = {"bound": "hbm", "kernel": "gemv_mfma_kernel<IQ2_KS,4096> (gate/up dispatch)",
                 "achieved": gu["decode"]["gb_per_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gu["decode"]["gb_per_s"] / HBM_PEAK_GBS, 4),
                 "per_launch_us": gu["decode"]["median_us"], "bytes_per_launch": gu["bytes_per_dispatch"],
-                "traffic": None}
+                # HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE passes over `--probe`,
+                # each calibrated on a plain copy of known size
+                "traffic": traffic, "traffic_source": traffic_file.name if traffic else None}
     line = {
         "metric": "routed decode achieved HBM GB/s (IQ2_KS, 256 experts, top-6, 1 token: gate+up and down)",
         "value": round(head["gb_per_s"], 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(head["ms_per_step"], 5), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "scaling": "weak", "vs_baseline": None, "dtype": "i8",
         "data": "synthetic: N(0,0.02) rows, U(0.1,1) imatrix, quantized by the package codec "
                 f"({args.distinct} distinct experts per projection, row-rotated to 256 distinct stacks)",
         "config": {"workload": "IQ2_KS routed decode, 256 experts, top-6, 1 token, gate/up [2048x4096] x2 "
