@@ -122,6 +122,11 @@ __device__ __forceinline__ uint32_t quad_xor(uint32_t v) {
     return uint32_t(__builtin_amdgcn_mov_dpp(int(v), ctrl, 0xF, 0xF, false));
 }
 
+// The value of lane 7 - (l % 8) of l's half-row of 8 lanes (DPP row_half_mirror).
+__device__ __forceinline__ uint32_t half_row_mirror(uint32_t v) {
+    return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x141, 0xF, 0xF, false));
+}
+
 __device__ __forceinline__ int digits_sum(int4_t d) { return d.x + (d.y << 8) + (d.z << 16); }
 
 // IQ1_S_R4's grid expanded to int8 weights 8 * (g + 1/8) = 8g + 1, eight per
@@ -180,7 +185,14 @@ struct Gemv2Smem {
     float part[Gemv2Shape<N>::KS][4][kGroupRows];
     int fsum[IQ1 ? N / 32 : 1];
     uint2_t b8[IQ1 ? IQK_IQ1S_GRID_SIZE : 1];
+    uint2_t ktab[MEMBER == IQ2_K ? 32 : 1];
+    float fw[MEMBER == IQ2_K ? N / 16 : 1];
 };
+
+// Activation exponent block: 64 elements for IQ2_K (a lane group's span of
+// a super-block, so its four words share one exponent), 32 otherwise.
+template <int MEMBER>
+constexpr int kExpBlock = MEMBER == IQ2_K ? 64 : 32;
 
 // Activations (fp16) -> balanced byte planes of 16-element words, in the
 // byte order the member's B operand uses.  Thread tid converts 8 activations
@@ -190,11 +202,14 @@ struct Gemv2Smem {
 //     of the fp16 pairs 2t+hp;
 //   natural (IQ1_S_R4): dword s byte t is element 4s+t, so the thread takes
 //     elements 8hp..8hp+7, the pairs 4hp..4hp+3.
-// With `fsum`, each 32-element block's integer sum(f) lands there too; with
-// ZERO_SPAN, the kWaveK bytes after the planes are cleared.
-template <int N, bool TRANSPOSED, bool ZERO_SPAN>
-__device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, int *fsum, int tid, uint4_t x0,
-                                                  uint4_t x1) {
+// One exponent E covers BLOCK (32 or 64) consecutive elements, 2^-E lands in
+// sbs[element / BLOCK].  With `fsum` / `fword`, each 32-element block's /
+// 16-element word's sum(f) lands there too; with ZERO_SPAN, the kWaveK bytes
+// after the planes are cleared.
+template <int N, bool TRANSPOSED, bool ZERO_SPAN, int BLOCK>
+__device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, int *fsum, float *fword, int tid,
+                                                  uint4_t x0, uint4_t x1) {
+    static_assert(BLOCK == 32 || BLOCK == 64, "4 or 8 threads per exponent block");
     const uint32_t wd = uint32_t(tid) >> 1, hp = uint32_t(tid) & 1u;
     if (ZERO_SPAN && tid < kWaveK / 16)
         *reinterpret_cast<uint4_t *>(dig + 3 * kPlaneStride<N> + 16 * tid) = uint4_t{0u, 0u, 0u, 0u};
@@ -208,6 +223,7 @@ __device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, int 
     uint32_t mx = max(uint32_t(m2.x), uint32_t(m2.y));
     mx = max(mx, quad_xor<1>(mx));  // the 4 threads of a 32-element block
     mx = max(mx, quad_xor<2>(mx));
+    if constexpr (BLOCK == 64) mx = max(mx, half_row_mirror(mx));  // the 8 of a 64-element block
     const bool finite = mx < 0x7c00u;
     // E so that max|x| * 2^E lies in [2^19, 2^20)
     const float amax = finite ? half_bits_to_float(mx) : 0.f;
@@ -239,14 +255,15 @@ __device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, int 
             (t < 2 ? u0 : u1)[e + 1] = bhi[t];
         }
     }
-    if (fsum) {  // sum(f) of the block (mod 2^32, exact: |sum| < 2^26)
+    if (fsum || fword) {  // sums of f (mod 2^32, exact: |sum| < 2^26)
         uint32_t f = 0;
 #pragma unroll
         for (int t = 0; t < 4; ++t) f += blo[t] + bhi[t];
         f -= 8u * 0x808080u;
-        f += quad_xor<1>(f);
-        f += quad_xor<2>(f);
-        if ((tid & 3) == 0) fsum[tid >> 2] = int(f);
+        f += quad_xor<1>(f);  // the 16-element word
+        if (fword && (tid & 1) == 0) fword[tid >> 1] = float(int(f));
+        f += quad_xor<2>(f);  // the 32-element block
+        if (fsum && (tid & 3) == 0) fsum[tid >> 2] = int(f);
     }
     uint32_t l0, l1, l2, h0, h1, h2;
     byte_planes(u0, l0, l1, l2);
@@ -255,7 +272,8 @@ __device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, int 
     *reinterpret_cast<uint2_t *>(dig + 0 * kPlaneStride<N> + off) = uint2_t{l0, h0};
     *reinterpret_cast<uint2_t *>(dig + 1 * kPlaneStride<N> + off) = uint2_t{l1, h1};
     *reinterpret_cast<uint2_t *>(dig + 2 * kPlaneStride<N> + off) = uint2_t{l2, h2};
-    if ((tid & 3) == 0) sbs[tid >> 2] = finite ? __uint_as_float(uint32_t(127 - E) << 23) : __builtin_nanf("");
+    if ((tid & (BLOCK / 8 - 1)) == 0)
+        sbs[tid / (BLOCK / 8)] = finite ? __uint_as_float(uint32_t(127 - E) << 23) : __builtin_nanf("");
 }
 
 // -- per-member lane state: loads, floor hash, and the decode ---------------------
@@ -338,8 +356,16 @@ struct LaneIq2k {
         return h;
     }
 
-    // sub-blocks 16s+4g+j (16 weights, word j of q[s]); d per super-block s
-    __device__ __forceinline__ float decode(const uint8_t *abase, const float *sbs, int g) const {
+    // sub-blocks 16s+4g+j (16 weights, word j of q[s]); d per super-block s.
+    // The scale index goes into the weights: with v = 2u + off,
+    // u in (-12, -3, 4, 12) and off = -7 (base alphabet) or -2 (shifted),
+    // idx * v = 2 (idx u) + idx off, and idx u fits int8, so the MFMA's B is a
+    // per-word pool idx * u and its D accumulates over the lane's four words
+    // of a super-block, which share one activation exponent.  The constant
+    // part idx * off * sum(f) takes one fma per word from the word's integer
+    // activation sum fw.  A lane folds once per super-block.
+    __device__ __forceinline__ float decode(const uint8_t *abase, const float *sbs, const float *fw,
+                                            const uint2_t *ktab, int g) const {
         // this lane's scale word of super-block s: u16 4s+g of the wavefront's 16
         const bool gh = (g >> 1) != 0;
         const int sh16 = 16 * (g & 1);
@@ -348,31 +374,54 @@ struct LaneIq2k {
         // alphabet bits of super-block s: byte 2s + g/2 of ex, bits 4(g%2) + j
         const int exs = 8 * (g >> 1) + 4 * (g & 1);
         const uint32_t exg[2] = {ex.x >> exs, ex.y >> exs};
-        float acc = 0.f, part = 0.f;
-        int4_t Dp;
+        float acc = 0.f, offp = 0.f;
+        int4_t Wp;
 #pragma unroll
-        for (int w = 0; w <= 16; ++w) {  // word w = 4s + j; fold word w-1 while w's MFMA runs
-            int4_t D;
-            if (w < 16) {
-                const int s = w >> 2, j = w & 3;
-                const uint32_t pool = pick_pool(exg[s >> 1], 16 * (s & 1) + j, kV8Base, kV8Shift);
-                D = mfma(read_a_all(abase + 256 * s + 16 * j), codes_to_i8(q[s][j], pool), int4_t{0, 0, 0, 0});
-            }
-            if (w > 0) {
-                const int s = (w - 1) >> 2, j = (w - 1) & 3;
-                const float up = sbs[8 * s + 2 * g + (j >> 1)];
-                const int idx = int((scw[s] >> (4 * j)) & 15u) - 8;
-                part = fmaf(float(digits_sum(Dp)), float(idx) * up, part);
-                if (j == 3) {
-                    acc = fmaf(half_bits_to_float((dv[s >> 1] >> (16 * (s & 1))) & 0xffffu), part, acc);
-                    part = 0.f;
+        for (int s = 0; s <= 4; ++s) {
+            int4_t W = {0, 0, 0, 0};
+            float off = 0.f;
+            if (s < 4) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t nib = (scw[s] >> (4 * j)) & 15u;
+                    const uint32_t alpha = (exg[s >> 1] >> (16 * (s & 1) + j)) & 1u;
+                    const uint2_t e = ktab[alpha * 16 + nib];
+                    W = mfma(read_a_all(abase + 256 * s + 16 * j), codes_to_i8(q[s][j], e.x), W);
+                    off = fmaf(__uint_as_float(e.y), fw[16 * s + 4 * g + j], off);
                 }
             }
-            if (w < 16) Dp = D;
+            if (s > 0) {  // fold the previous super-block while this one's MFMAs run
+                const int sp = s - 1;
+                const float sum = fmaf(float(Wp.z), 65536.f, fmaf(float(Wp.y), 256.f, float(Wp.x)));
+                const float d = half_bits_to_float((dv[sp >> 1] >> (16 * (sp & 1))) & 0xffffu);
+                acc = fmaf(fmaf(2.f, sum, offp), d * sbs[4 * sp + g], acc);
+            }
+            if (s < 4) { Wp = W; offp = off; }
         }
         return acc;
     }
 };
+
+// IQ2_K's per-word factors, by (alphabet << 4 | scale nibble): the int8 pool
+// idx * u_c (u = -12, -3, 4, 12) and the float idx * off, with idx =
+// nibble - 8 and off = -7 (base alphabet) or -2 (shifted).
+struct Iq2kTable {
+    uint32_t w[2 * 32];
+};
+
+constexpr Iq2kTable make_iq2k_table() {
+    Iq2kTable t{};
+    constexpr int u[4] = {-12, -3, 4, 12};
+    for (int alpha = 0; alpha < 2; ++alpha)
+        for (int nib = 0; nib < 16; ++nib) {
+            const int idx = nib - 8, off = alpha ? -2 : -7, e = alpha * 16 + nib;
+            for (int c = 0; c < 4; ++c) t.w[2 * e] |= uint32_t(uint8_t(int8_t(idx * u[c]))) << (8 * c);
+            t.w[2 * e + 1] = __builtin_bit_cast(uint32_t, float(idx * off));
+        }
+    return t;
+}
+
+__constant__ const Iq2kTable kIq2kTab = make_iq2k_table();
 
 // IQ1_S_R4 streams: qs u32 [N/32] (4 index bytes per 32-weight block),
 // qh u16 [N/32], dv f16.
@@ -468,13 +517,17 @@ void gemv_mfma_kernel(Gemv2Args a) {
 #pragma unroll
     for (int i = 0; i < GRID_CHUNKS; ++i)
         gridv[i] = reinterpret_cast<const uint4_t *>(kIq1B8.w)[tid + i * S::THREADS];
+    constexpr bool KTAB = MEMBER == IQ2_K && !FLOOR;
+    uint2_t ktv = {0u, 0u};
+    if (KTAB && tid < 32) ktv = reinterpret_cast<const uint2_t *>(kIq2kTab.w)[tid];
 
-    const uint32_t e = a.sel[m];
+    // An id beyond the stack reads expert 0 (in bounds) and writes NaN rows.
+    // No early exit: a branch here would let the compiler sink the loads
+    // above behind the wait for the id.
+    const uint32_t e_raw = a.sel[m];
+    const bool valid = e_raw < a.num_experts;  // uniform per workgroup
+    const uint32_t e = valid ? e_raw : 0u;
     uint16_t *ygroup = a.y + size_t(m) * a.out_features + rowg;
-    if (e >= a.num_experts) {  // uniform per workgroup
-        if (tid < kGroupRows) ygroup[tid] = kHalfNaN;
-        return;
-    }
     const uint32_t row = e * a.out_features + rowg + 16 * tile + n;
     LaneOf<MEMBER, N> lane;
     lane.load(a, row, kq, g);
@@ -487,7 +540,9 @@ void gemv_mfma_kernel(Gemv2Args a) {
     } else {
 #pragma unroll
         for (int i = 0; i < GRID_CHUNKS; ++i) reinterpret_cast<uint4_t *>(sm.b8)[tid + i * S::THREADS] = gridv[i];
-        stage_activations<N, !IQ1, !kMaskedA<MEMBER>>(sm.dig, sm.sbs, IQ1 ? sm.fsum : nullptr, tid, x0, x1);
+        if (KTAB && tid < 32) sm.ktab[tid] = ktv;
+        stage_activations<N, !IQ1, !kMaskedA<MEMBER>, kExpBlock<MEMBER>>(
+            sm.dig, sm.sbs, IQ1 ? sm.fsum : nullptr, MEMBER == IQ2_K ? sm.fw : nullptr, tid, x0, x1);
         __syncthreads();
         const int ai = l & 15;  // this lane's A row
         const bool data = (ai >> 2) == g && (ai & 3) < 3;
@@ -500,7 +555,7 @@ void gemv_mfma_kernel(Gemv2Args a) {
         else if constexpr (MEMBER == IQ2_KS)
             acc = lane.decode(abase, data, sbs, g);
         else
-            acc = lane.decode(abase, sbs, g);
+            acc = lane.decode(abase, sm.sbs + (kWaveK / 64) * kq, sm.fw + (kWaveK / 16) * kq, sm.ktab, g);
     }
     sm.part[kq][g][16 * tile + n] = acc;
     __syncthreads();
@@ -508,7 +563,7 @@ void gemv_mfma_kernel(Gemv2Args a) {
         float sum = 0.f;
 #pragma unroll
         for (int k = 0; k < KS; ++k) sum += (sm.part[k][0][tid] + sm.part[k][1][tid]) + (sm.part[k][2][tid] + sm.part[k][3][tid]);
-        ygroup[tid] = uint16_t(float_to_half_bits(sum));
+        ygroup[tid] = valid ? uint16_t(float_to_half_bits(sum)) : kHalfNaN;
     }
 }
 
