@@ -181,12 +181,12 @@ template <int MEMBER, int N>
 struct Gemv2Smem {
     static constexpr bool IQ1 = MEMBER == IQ1_S_R4;
     uint8_t dig[3 * kPlaneStride<N> + (kMaskedA<MEMBER> ? 0 : kWaveK)] __attribute__((aligned(16)));
-    float sbs[N / 32];
+    float sbs[N / 32] __attribute__((aligned(16)));
     float part[Gemv2Shape<N>::KS][4][kGroupRows];
-    int fsum[IQ1 ? N / 32 : 1];
+    int fsum[IQ1 ? N / 32 : 4] __attribute__((aligned(16)));
     uint2_t b8[IQ1 ? IQK_IQ1S_GRID_SIZE : 1];
     uint2_t ktab[MEMBER == IQ2_K ? 32 : 1];
-    float fw[MEMBER == IQ2_K ? N / 16 : 1];
+    float fw[MEMBER == IQ2_K ? N / 16 : 4] __attribute__((aligned(16)));
 };
 
 // Activation exponent block: 64 elements for IQ2_K (a lane group's span of
@@ -305,6 +305,9 @@ struct LaneIq2ks {
         const uint32_t hbg = hb >> (2 * g), abg = ab >> (2 * g);
         const uint32_t scg[4] = {sc.x >> (8 * g), sc.y >> (8 * g), sc.z >> (8 * g), sc.w >> (8 * g)};
         float acc = 0.f;
+        float2 upv[4];  // 2^-E of sub-blocks 8s+2g, 8s+2g+1, read before the loop
+#pragma unroll
+        for (int s = 0; s < 4; ++s) upv[s] = *reinterpret_cast<const float2 *>(sbs + 8 * s + 2 * g);
         int4_t Dp[2], A[4] = {};
 #pragma unroll
         for (int s = 0; s <= 4; ++s) {
@@ -322,7 +325,7 @@ struct LaneIq2ks {
                 const int sp = s - 1;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    const float up = sbs[8 * sp + 2 * g + h];
+                    const float up = h ? upv[sp].y : upv[sp].x;
                     const int idx = int(((scg[sp] >> (4 * h)) & 15u) | (((hbg >> (8 * sp + h)) & 1u) << 4)) - 16;
                     acc = fmaf(float(digits_sum(Dp[h])), float(idx) * up, acc);
                 }
@@ -375,6 +378,13 @@ struct LaneIq2k {
         const int exs = 8 * (g >> 1) + 4 * (g & 1);
         const uint32_t exg[2] = {ex.x >> exs, ex.y >> exs};
         float acc = 0.f, offp = 0.f;
+        float upk[4];  // 2^-E and word sums of this lane's spans, read before the loop
+        float4 fwv[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            upk[s] = sbs[4 * s + g];
+            fwv[s] = *reinterpret_cast<const float4 *>(fw + 16 * s + 4 * g);
+        }
         int4_t Wp;
 #pragma unroll
         for (int s = 0; s <= 4; ++s) {
@@ -387,14 +397,14 @@ struct LaneIq2k {
                     const uint32_t alpha = (exg[s >> 1] >> (16 * (s & 1) + j)) & 1u;
                     const uint2_t e = ktab[alpha * 16 + nib];
                     W = mfma(read_a_all(abase + 256 * s + 16 * j), codes_to_i8(q[s][j], e.x), W);
-                    off = fmaf(__uint_as_float(e.y), fw[16 * s + 4 * g + j], off);
+                    off = fmaf(__uint_as_float(e.y), fwv[s][j], off);
                 }
             }
             if (s > 0) {  // fold the previous super-block while this one's MFMAs run
                 const int sp = s - 1;
                 const float sum = fmaf(float(Wp.z), 65536.f, fmaf(float(Wp.y), 256.f, float(Wp.x)));
                 const float d = half_bits_to_float((dv[sp >> 1] >> (16 * (sp & 1))) & 0xffffu);
-                acc = fmaf(fmaf(2.f, sum, offp), d * sbs[4 * sp + g], acc);
+                acc = fmaf(fmaf(2.f, sum, offp), d * upk[sp], acc);
             }
             if (s < 4) { Wp = W; offp = off; }
         }
@@ -451,6 +461,13 @@ struct LaneIq1s {
     __device__ __forceinline__ float decode(const uint8_t *abase, bool data, const float *sbs, const int *fsum,
                                             const uint2_t *b8, int g) const {
         float acc = 0.f;
+        float4 upv[2];  // 2^-E and sum(f) of blocks 16i+4g+b, read before the loop
+        int4_t fsv[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            upv[i] = *reinterpret_cast<const float4 *>(sbs + 16 * i + 4 * g);
+            fsv[i] = *reinterpret_cast<const int4_t *>(fsum + 16 * i + 4 * g);
+        }
         int4_t Dp, A[4] = {};
         uint32_t hp = 0;
 #pragma unroll
@@ -472,11 +489,11 @@ struct LaneIq1s {
                 }
             }
             if (c > 0) {
-                const int cp = c - 1, blk = 16 * (cp >> 2) + 4 * g + (cp & 3);
+                const int cp = c - 1;
                 const int neg = int(hp >> 15);
-                const int sint = digits_sum(Dp) - ((2 * fsum[blk]) & -neg);
+                const int sint = digits_sum(Dp) - ((2 * fsv[cp >> 2][cp & 3]) & -neg);
                 const float ls = float(2 * ((hp >> 12) & 7u) + 1);
-                acc = fmaf(float(sint), ls * sbs[blk], acc);
+                acc = fmaf(float(sint), ls * upv[cp >> 2][cp & 3], acc);
             }
             if (c < 8) { Dp = D; hp = hw; }
         }
