@@ -69,7 +69,7 @@ constexpr uint32_t kV8Base = 0x1101F3E1u;   // int8 -31, -13, 1, 17
 constexpr uint32_t kV8Shift = 0x1606F8E6u;  // int8 -26, -8, 6, 22
 constexpr uint32_t kG8Plus = 0x000901F9u;   // int8 8(g + 1/8), g = -1, 0, 1
 constexpr uint32_t kG8Minus = 0x0007FFF7u;  // int8 8(g - 1/8)
-constexpr int kWaveK = 1024;                // reduction elements per wavefront
+constexpr int kWaveK = 1024;                // reduction elements per wavefront (default)
 constexpr int kGroupRows = 32;              // rows per workgroup
 
 // Byte planes sit 16 bytes more than N apart, so one lane group's three
@@ -77,11 +77,17 @@ constexpr int kGroupRows = 32;              // rows per workgroup
 template <int N>
 constexpr int kPlaneStride = N + 16;
 
-template <int N>
+// Work split of one workgroup: 32 rows, KS wavefronts of WK reduction
+// elements per 16 rows.  IQ1_S_R4's 2048-wide down projection uses 512-wide
+// slices, so its workgroups are eight wavefronts like the others and a CU
+// holds three copies of the LDS grid instead of six.
+template <int MEMBER, int N>
 struct Gemv2Shape {
-    static constexpr int KS = N / kWaveK;  // wavefronts per 16 rows
+    static constexpr int WK = MEMBER == IQ1_S_R4 && N == 2048 ? 512 : kWaveK;
+    static constexpr int KS = N / WK;      // wavefronts per 16 rows
     static constexpr int THREADS = 64 * 2 * KS;
-    static_assert(N / 8 == THREADS, "one thread per 8 activations");
+    static constexpr int UNITS = N / 8;    // activation staging units of 8 elements
+    static_assert(THREADS >= UNITS && UNITS % 64 == 0, "whole wavefronts stage the activations");
     static_assert(IQK_IQ1S_GRID_SIZE / 2 % THREADS == 0, "whole uint4 grid chunks per thread");
 };
 
@@ -180,9 +186,9 @@ constexpr bool kMaskedA = MEMBER != IQ2_K;
 template <int MEMBER, int N>
 struct Gemv2Smem {
     static constexpr bool IQ1 = MEMBER == IQ1_S_R4;
-    uint8_t dig[3 * kPlaneStride<N> + (kMaskedA<MEMBER> ? 0 : kWaveK)] __attribute__((aligned(16)));
+    uint8_t dig[3 * kPlaneStride<N> + (kMaskedA<MEMBER> ? 0 : Gemv2Shape<MEMBER, N>::WK)] __attribute__((aligned(16)));
     float sbs[N / 32] __attribute__((aligned(16)));
-    float part[Gemv2Shape<N>::KS][4][kGroupRows];
+    float part[Gemv2Shape<MEMBER, N>::KS][4][kGroupRows];
     int fsum[IQ1 ? N / 32 : 4] __attribute__((aligned(16)));
     uint2_t b8[IQ1 ? IQK_IQ1S_GRID_SIZE : 1];
     uint2_t ktab[MEMBER == IQ2_K ? 32 : 1];
@@ -204,14 +210,14 @@ constexpr int kExpBlock = MEMBER == IQ2_K ? 64 : 32;
 //     elements 8hp..8hp+7, the pairs 4hp..4hp+3.
 // One exponent E covers BLOCK (32 or 64) consecutive elements, 2^-E lands in
 // sbs[element / BLOCK].  With `fsum` / `fword`, each 32-element block's /
-// 16-element word's sum(f) lands there too; with ZERO_SPAN, the kWaveK bytes
+// 16-element word's sum(f) lands there too; with ZERO_SPAN, the WK bytes
 // after the planes are cleared.
-template <int N, bool TRANSPOSED, bool ZERO_SPAN, int BLOCK>
+template <int N, bool TRANSPOSED, bool ZERO_SPAN, int BLOCK, int WK>
 __device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, int *fsum, float *fword, int tid,
                                                   uint4_t x0, uint4_t x1) {
     static_assert(BLOCK == 32 || BLOCK == 64, "4 or 8 threads per exponent block");
     const uint32_t wd = uint32_t(tid) >> 1, hp = uint32_t(tid) & 1u;
-    if (ZERO_SPAN && tid < kWaveK / 16)
+    if (ZERO_SPAN && tid < WK / 16)
         *reinterpret_cast<uint4_t *>(dig + 3 * kPlaneStride<N> + 16 * tid) = uint4_t{0u, 0u, 0u, 0u};
     const uint4_t xv = hp ? x1 : x0;
     const uint32_t xp[4] = {TRANSPOSED ? (hp ? x0.y : x0.x) : xv.x, TRANSPOSED ? (hp ? x0.w : x0.z) : xv.y,
@@ -435,24 +441,28 @@ __constant__ const Iq2kTable kIq2kTab = make_iq2k_table();
 
 // IQ1_S_R4 streams: qs u32 [N/32] (4 index bytes per 32-weight block),
 // qh u16 [N/32], dv f16.
-template <int N>
+template <int N, int WK>
 struct LaneIq1s {
-    uint4_t qv[2];
-    uint2_t qh[2];
+    static constexpr int NI = WK / 512;  // 512-weight spans per wavefront
+    uint4_t qv[NI];
+    uint2_t qh[NI];
     uint32_t dvb;
 
     __device__ __forceinline__ void load(const Gemv2Args &a, uint32_t row, uint32_t kq, uint32_t g) {
-        const uint32_t qo = row * (N / 8) + 128 * kq + 16 * g, ho = row * (N / 16) + 64 * kq + 8 * g;
-        qh[0] = *reinterpret_cast<const uint2_t *>(bytes(a.s1) + ho);
-        qh[1] = *reinterpret_cast<const uint2_t *>(bytes(a.s1) + (ho + 32));
+        const uint32_t qo = row * (N / 8) + (WK / 8) * kq + 16 * g, ho = row * (N / 16) + (WK / 16) * kq + 8 * g;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) qh[i] = *reinterpret_cast<const uint2_t *>(bytes(a.s1) + (ho + 32 * i));
         dvb = *reinterpret_cast<const uint16_t *>(bytes(a.s2) + 2 * row);
-        qv[0] = load_u4(bytes(a.s0) + qo);
-        qv[1] = load_u4(bytes(a.s0) + (qo + 64));
+#pragma unroll
+        for (int i = 0; i < NI; ++i) qv[i] = load_u4(bytes(a.s0) + (qo + 64 * i));
     }
 
     __device__ __forceinline__ uint32_t hash() const {
-        return qv[0].x + 3u * qv[0].y + 5u * qv[0].z + 7u * qv[0].w + 11u * qv[1].x + 13u * qv[1].y +
-               17u * qv[1].z + 19u * qv[1].w + 59u * (qh[0].x + qh[0].y) + 61u * (qh[1].x + qh[1].y) + 67u * dvb;
+        uint32_t h = 67u * dvb;
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            h += (2 * i + 3) * (qv[i].x + 3u * qv[i].y + 5u * qv[i].z + 7u * qv[i].w) + 59u * (qh[i].x + 7u * qh[i].y);
+        return h;
     }
 
     // blocks 16i+4g+b (32 weights: index bytes of dword b of qv[i], qh word b
@@ -461,20 +471,20 @@ struct LaneIq1s {
     __device__ __forceinline__ float decode(const uint8_t *abase, bool data, const float *sbs, const int *fsum,
                                             const uint2_t *b8, int g) const {
         float acc = 0.f;
-        float4 upv[2];  // 2^-E and sum(f) of blocks 16i+4g+b, read before the loop
-        int4_t fsv[2];
+        float4 upv[NI];  // 2^-E and sum(f) of blocks 16i+4g+b, read before the loop
+        int4_t fsv[NI];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < NI; ++i) {
             upv[i] = *reinterpret_cast<const float4 *>(sbs + 16 * i + 4 * g);
             fsv[i] = *reinterpret_cast<const int4_t *>(fsum + 16 * i + 4 * g);
         }
         int4_t Dp, A[4] = {};
         uint32_t hp = 0;
 #pragma unroll
-        for (int c = 0; c <= 8; ++c) {  // block c = 4i + b
+        for (int c = 0; c <= 4 * NI; ++c) {  // block c = 4i + b
             int4_t D;
             uint32_t hw = 0;
-            if (c < 8) {
+            if (c < 4 * NI) {
                 const int i = c >> 2, b = c & 3;
                 if ((b & 1) == 0) read_a(A, abase + 512 * i + 32 * b, data);  // blocks b, b+1
                 const uint32_t qw = qv[i][b];
@@ -495,7 +505,7 @@ struct LaneIq1s {
                 const float ls = float(2 * ((hp >> 12) & 7u) + 1);
                 acc = fmaf(float(sint), ls * upv[cp >> 2][cp & 3], acc);
             }
-            if (c < 8) { Dp = D; hp = hw; }
+            if (c < 4 * NI) { Dp = D; hp = hw; }
         }
         return acc * (0.125f * half_bits_to_float(dvb));
     }
@@ -503,15 +513,16 @@ struct LaneIq1s {
 
 template <int MEMBER, int N>
 using LaneOf = std::conditional_t<MEMBER == IQ2_KS, LaneIq2ks<N>,
-                                  std::conditional_t<MEMBER == IQ2_K, LaneIq2k<N>, LaneIq1s<N>>>;
+                                  std::conditional_t<MEMBER == IQ2_K, LaneIq2k<N>,
+                                                     LaneIq1s<N, Gemv2Shape<MEMBER, N>::WK>>>;
 
 // Six wavefronts per SIMD: three workgroups of eight (N = 4096) or six of
 // four (N = 2048) per CU, so a 1-token routed decode's 768 workgroups are
 // resident at once.
 template <int MEMBER, int N, bool FLOOR>
-__global__ __launch_bounds__(Gemv2Shape<N>::THREADS) __attribute__((amdgpu_waves_per_eu(6)))
+__global__ __launch_bounds__((Gemv2Shape<MEMBER, N>::THREADS)) __attribute__((amdgpu_waves_per_eu(6)))
 void gemv_mfma_kernel(Gemv2Args a) {
-    using S = Gemv2Shape<N>;
+    using S = Gemv2Shape<MEMBER, N>;
     constexpr int KS = S::KS;
     __shared__ Gemv2Smem<MEMBER, N> sm;
 
@@ -527,7 +538,12 @@ void gemv_mfma_kernel(Gemv2Args a) {
     // expert id, and vector loads retire in order, so staging them waits for
     // none of the stream bytes issued after them.
     const uint32_t xo = tok * (2 * N) + 32 * (uint32_t(tid) >> 1);
-    const uint4_t x0 = load_u4(bytes(a.x) + xo), x1 = load_u4(bytes(a.x) + (xo + 16));
+    const bool stager = tid < S::UNITS;  // uniform per wavefront
+    uint4_t x0 = {0u, 0u, 0u, 0u}, x1 = {0u, 0u, 0u, 0u};
+    if (stager) {
+        x0 = load_u4(bytes(a.x) + xo);
+        x1 = load_u4(bytes(a.x) + (xo + 16));
+    }
     constexpr bool IQ1 = MEMBER == IQ1_S_R4;
     constexpr int GRID_CHUNKS = IQ1 && !FLOOR ? IQK_IQ1S_GRID_SIZE / 2 / S::THREADS : 0;  // uint4 per thread
     uint4_t gridv[GRID_CHUNKS > 0 ? GRID_CHUNKS : 1];
@@ -558,21 +574,22 @@ void gemv_mfma_kernel(Gemv2Args a) {
 #pragma unroll
         for (int i = 0; i < GRID_CHUNKS; ++i) reinterpret_cast<uint4_t *>(sm.b8)[tid + i * S::THREADS] = gridv[i];
         if (KTAB && tid < 32) sm.ktab[tid] = ktv;
-        stage_activations<N, !IQ1, !kMaskedA<MEMBER>, kExpBlock<MEMBER>>(
-            sm.dig, sm.sbs, IQ1 ? sm.fsum : nullptr, MEMBER == IQ2_K ? sm.fw : nullptr, tid, x0, x1);
+        if (stager)
+            stage_activations<N, !IQ1, !kMaskedA<MEMBER>, kExpBlock<MEMBER>, S::WK>(
+                sm.dig, sm.sbs, IQ1 ? sm.fsum : nullptr, MEMBER == IQ2_K ? sm.fw : nullptr, tid, x0, x1);
         __syncthreads();
         const int ai = l & 15;  // this lane's A row
         const bool data = (ai >> 2) == g && (ai & 3) < 3;
         constexpr int LANE_K = IQ1 ? 128 : 64;
-        const uint8_t *abase = sm.dig + (data || kMaskedA<MEMBER> ? (ai & 3) * kPlaneStride<N> + kWaveK * kq + LANE_K * g
+        const uint8_t *abase = sm.dig + (data || kMaskedA<MEMBER> ? (ai & 3) * kPlaneStride<N> + S::WK * kq + LANE_K * g
                                                                  : 3 * kPlaneStride<N>);
-        const float *sbs = sm.sbs + (kWaveK / 32) * kq;
+        const float *sbs = sm.sbs + (S::WK / 32) * kq;
         if constexpr (IQ1)
-            acc = lane.decode(abase, data, sbs, sm.fsum + (kWaveK / 32) * kq, sm.b8, g);
+            acc = lane.decode(abase, data, sbs, sm.fsum + (S::WK / 32) * kq, sm.b8, g);
         else if constexpr (MEMBER == IQ2_KS)
             acc = lane.decode(abase, data, sbs, g);
         else
-            acc = lane.decode(abase, sm.sbs + (kWaveK / 64) * kq, sm.fw + (kWaveK / 16) * kq, sm.ktab, g);
+            acc = lane.decode(abase, sm.sbs + (S::WK / 64) * kq, sm.fw + (S::WK / 16) * kq, sm.ktab, g);
     }
     sm.part[kq][g][16 * tile + n] = acc;
     __syncthreads();
@@ -587,10 +604,11 @@ void gemv_mfma_kernel(Gemv2Args a) {
 template <int MEMBER, bool FLOOR>
 int launch_gemv_mfma(int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t st) {
     const dim3 grid{a.out_features / kGroupRows, a.pairs_per_row, mats / a.pairs_per_row};
+    const dim3 block4096{uint32_t(Gemv2Shape<MEMBER, 4096>::THREADS)}, block2048{uint32_t(Gemv2Shape<MEMBER, 2048>::THREADS)};
     if (n == 4096)
-        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 4096, FLOOR>), grid, dim3{Gemv2Shape<4096>::THREADS}, 0, st, a);
+        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 4096, FLOOR>), grid, block4096, 0, st, a);
     else
-        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 2048, FLOOR>), grid, dim3{Gemv2Shape<2048>::THREADS}, 0, st, a);
+        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 2048, FLOOR>), grid, block2048, 0, st, a);
     return record_launch(hipGetLastError());
 }
 
