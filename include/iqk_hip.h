@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define IQK_HIP_ABI_VERSION 1
+#define IQK_HIP_ABI_VERSION 2
 
 #define IQK_MEMBER_IQ2_KS 0
 #define IQK_MEMBER_IQ2_K 1
@@ -74,6 +74,31 @@ int iqk_gemv_floor(int member, int64_t in_features, int64_t out_features, int64_
                    const uint32_t *sel, uint32_t pairs_per_row, uint32_t mats,
                    void *y, void *stream);
 
+// Decode GEMV over expert-sorted pairs, one workgroup per pair (replaces
+// gemv_sorted_kernel + IqkSwitchLinear.gemv_sorted,
+// src/mlx_iqk/kernels.py:404-482, 813-832, src/mlx_iqk/nn.py:273-299):
+//   y[p, r] = fp16( sum_k W[sorted_ids[p]][r][k] * x[toks[p]][k] )
+// x: f16 [n_x_rows, in_features]; sorted_ids, toks: u32 [mats] (device);
+// y: f16 [mats, out_features].  Each output element is iqk_gemv's, bit for
+// bit, so y is iqk_gemv's rows in the caller's sorted order.  A pair whose
+// toks entry is >= n_x_rows, or whose id is >= num_experts, gets a NaN row.
+// IQK_MEMBER_IQ2_KS and IQK_MEMBER_IQ2_K only (IQ1_S_R4: IQK_ERR_MEMBER).
+int iqk_gemv_sorted(int member, int64_t in_features, int64_t out_features, int64_t num_experts,
+                    const void *x, int64_t n_x_rows, const void *const *streams, int n_streams,
+                    const uint32_t *sorted_ids, const uint32_t *toks, uint32_t mats,
+                    void *y, void *stream);
+
+// The same contraction, one stream read per run of equal adjacent ids
+// (replaces gemv_union_kernel + IqkSwitchLinear.gemv_union,
+// src/mlx_iqk/kernels.py:484-578, 834-853, src/mlx_iqk/nn.py:301-333): the
+// workgroup of a run's first pair computes every pair of the run from one
+// read of the expert's rows.  Arguments, output and refusals as
+// iqk_gemv_sorted, and bit-identical to it.
+int iqk_gemv_union(int member, int64_t in_features, int64_t out_features, int64_t num_experts,
+                   const void *x, int64_t n_x_rows, const void *const *streams, int n_streams,
+                   const uint32_t *sorted_ids, const uint32_t *toks, uint32_t mats,
+                   void *y, void *stream);
+
 // Stacked-expert dequant producer (replaces dequant_kernel + dispatch,
 // src/mlx_iqk/kernels.py:855-869, src/mlx_iqk/nn.py:155-169):
 //   w[slot(e)][r][k] = fp16( d * float(index) * value )   bit-exact,
@@ -85,6 +110,19 @@ int iqk_dequant(int member, int64_t in_features, int64_t out_features, int64_t n
                 const void *const *streams, int n_streams,
                 const int32_t *slot_of_expert, int64_t n_slots,
                 void *w, void *stream);
+
+// The producer over out-row range [row_start, row_start + rows) (replaces
+// dequant_range_kernel + IqkSwitchLinear.dequantized_range,
+// src/mlx_iqk/kernels.py:679-758, 872-888, src/mlx_iqk/nn.py:171-201):
+//   w[slot(e)][r][k] = the full producer's w[slot(e)][row_start + r][k]
+// bit for bit, w: f16 [n_slots, rows, in_features], slots as iqk_dequant.
+// IQK_ERR_GEOMETRY unless 0 <= row_start, 0 < rows and
+// row_start + rows <= out_features.  iqk_dequant is the case row_start = 0,
+// rows = out_features.
+int iqk_dequant_rows(int member, int64_t in_features, int64_t out_features, int64_t num_experts,
+                     const void *const *streams, int n_streams, int64_t row_start, int64_t rows,
+                     const int32_t *slot_of_expert, int64_t n_slots,
+                     void *w, void *stream);
 
 // The producer's floor: identical loads and stores, decode deleted
 // (reference: bench/floors.py:179-220).
@@ -103,7 +141,8 @@ int iqk_dequant_floor(int member, int64_t in_features, int64_t out_features, int
 // y: f16 [n_slots, out_features]; group_offsets: u32 [n_groups + 1] (device,
 // non-decreasing, last = n_slots); x_rows, y_rows: u32 [n_slots] (device;
 // y_rows NULL = identity, else a permutation of [0, n_slots)).  Device-side
-// indices out of range are skipped, never dereferenced.
+// indices out of range are skipped, never dereferenced.  in_features % 32 == 0;
+// any out_features > 0.
 int iqk_grouped_gemm(int64_t in_features, int64_t out_features, int64_t n_groups, int64_t n_slots,
                      const void *x, int64_t n_x_rows, const void *w, const uint32_t *group_offsets,
                      const uint32_t *x_rows, const uint32_t *y_rows, void *y, void *stream);

@@ -34,6 +34,8 @@ struct DequantArgs {
     const int32_t *slot_of_expert;
     uint32_t num_experts;
     uint32_t out_features;
+    uint32_t row_start;  // first source row inside each expert
+    uint32_t rows;       // rows per expert written: w[slot][0..rows)
     uint32_t n_slots;
     uint16_t *w;
 };
@@ -172,17 +174,18 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t stage[256 * kStageDwords];
     static_assert(IQK_IQ1S_GRID_SIZE * 2 == 256 * 16, "one 16-byte grid chunk per thread");
     const uint64_t gid = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    const uint64_t row = gid / TPR;  // stacked source row
+    const uint64_t lin = gid / TPR;  // (expert, range row)
     const int lc = int(gid % TPR);
-    const uint32_t expert = uint32_t(row / a.out_features);
+    const uint32_t expert = uint32_t(lin / a.rows);
     const int32_t slot = expert < a.num_experts ? (a.slot_of_expert ? a.slot_of_expert[expert] : int32_t(expert)) : -1;
     const bool valid = slot >= 0 && uint32_t(slot) < a.n_slots;
     uint32_t out[32];
     uint16_t *dst = nullptr;
     RawChunk raw{};
     if (valid) {
-        const uint32_t r = uint32_t(row - uint64_t(expert) * a.out_features);
-        dst = a.w + (uint64_t(slot) * a.out_features + r) * N + 64 * lc;
+        const uint32_t r = uint32_t(lin - uint64_t(expert) * a.rows);
+        const uint64_t row = uint64_t(expert) * a.out_features + a.row_start + r;  // stacked source row
+        dst = a.w + (uint64_t(slot) * a.rows + r) * N + 64 * lc;
         raw = load_chunk<MEMBER, N>(a, row, lc);
     }
     if constexpr (MEMBER == IQ1_S_R4 && !FLOOR) {  // the grid, after the stream loads are in flight
@@ -217,7 +220,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
 
 template <int MEMBER, bool FLOOR>
 int launch_dequant(int64_t n, const DequantArgs &a, hipStream_t st) {
-    const uint64_t threads = uint64_t(a.num_experts) * a.out_features * uint64_t(n / 64);
+    const uint64_t threads = uint64_t(a.num_experts) * a.rows * uint64_t(n / 64);
     const uint64_t blocks = (threads + 255) / 256;
     if (blocks > 0x7fffffffull) return IQK_ERR_GEOMETRY;
     const dim3 grid{uint32_t(blocks)}, block{256};
@@ -228,11 +231,15 @@ int launch_dequant(int64_t n, const DequantArgs &a, hipStream_t st) {
     return record_launch(hipGetLastError());
 }
 
+// Every producer entry point: rows [row_start, row_start + rows) of each
+// selected expert into w[slot][0..rows).
 template <bool FLOOR>
 int dequant_entry(int member, int64_t n, int64_t out, int64_t num_experts, const void *const *streams,
-                  int n_streams, const int32_t *slot_of_expert, int64_t n_slots, void *w, void *stream) {
+                  int n_streams, int64_t row_start, int64_t rows, const int32_t *slot_of_expert, int64_t n_slots,
+                  void *w, void *stream) {
     const int g = iqk_check_dequant_geometry(member, n, out);
     if (g != IQK_OK) return g;
+    if (row_start < 0 || rows <= 0 || row_start + rows > out) return IQK_ERR_GEOMETRY;
     if (!w || !streams_ok(streams, n_streams, member)) return IQK_ERR_ARGUMENT;
     if (num_experts <= 0 || num_experts > 0xffffffffll || n_slots < 0 || n_slots > 0xffffffffll)
         return IQK_ERR_ARGUMENT;
@@ -245,6 +252,8 @@ int dequant_entry(int member, int64_t n, int64_t out, int64_t num_experts, const
     a.slot_of_expert = slot_of_expert;
     a.num_experts = uint32_t(num_experts);
     a.out_features = uint32_t(out);
+    a.row_start = uint32_t(row_start);
+    a.rows = uint32_t(rows);
     a.n_slots = uint32_t(n_slots);
     a.w = static_cast<uint16_t *>(w);
     hipStream_t st = as_stream(stream);
@@ -268,14 +277,21 @@ int iqk_check_dequant_geometry(int member, int64_t n, int64_t out) {
 
 int iqk_dequant(int member, int64_t n, int64_t out, int64_t num_experts, const void *const *streams,
                 int n_streams, const int32_t *slot_of_expert, int64_t n_slots, void *w, void *stream) {
-    return iqk::dequant_entry<false>(member, n, out, num_experts, streams, n_streams, slot_of_expert, n_slots,
-                                     w, stream);
+    return iqk::dequant_entry<false>(member, n, out, num_experts, streams, n_streams, 0, out, slot_of_expert,
+                                     n_slots, w, stream);
+}
+
+int iqk_dequant_rows(int member, int64_t n, int64_t out, int64_t num_experts, const void *const *streams,
+                     int n_streams, int64_t row_start, int64_t rows, const int32_t *slot_of_expert, int64_t n_slots,
+                     void *w, void *stream) {
+    return iqk::dequant_entry<false>(member, n, out, num_experts, streams, n_streams, row_start, rows,
+                                     slot_of_expert, n_slots, w, stream);
 }
 
 int iqk_dequant_floor(int member, int64_t n, int64_t out, int64_t num_experts, const void *const *streams,
                       int n_streams, const int32_t *slot_of_expert, int64_t n_slots, void *w, void *stream) {
-    return iqk::dequant_entry<true>(member, n, out, num_experts, streams, n_streams, slot_of_expert, n_slots,
-                                    w, stream);
+    return iqk::dequant_entry<true>(member, n, out, num_experts, streams, n_streams, 0, out, slot_of_expert,
+                                    n_slots, w, stream);
 }
 
 }  // extern "C"

@@ -12,7 +12,9 @@
 // worst case ceil(n_slots/BM) + n_groups M-tiles and surplus blocks exit.
 //
 // Tile.  256 threads, four wavefronts, BM x BN = 64 x 256; each wavefront
-// owns a 64 x 64 sub-tile as 4 x 4 v_mfma_f32_16x16x32_f16 tiles.  With both
+// owns a 64 x 64 sub-tile as 4 x 4 v_mfma_f32_16x16x32_f16 tiles.  Any
+// out_features works: a lane's B row is its D column, so columns at or beyond
+// out_features are neither loaded nor stored, lane by lane.  With both
 // operands k-contiguous (x rows and W rows), an MFMA operand fragment is 16
 // contiguous bytes per lane, loaded straight from global memory and reused
 // four times from registers.
@@ -96,8 +98,12 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a) {
         ap[i] = a.x + size_t(av[i] ? xrow : 0u) * a.K + lk;
     }
     const uint16_t *bp[4];
+    bool bv[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bp[j] = a.w + (size_t(g) * a.N + n0 + 16 * j + lr) * a.K + lk;
+    for (int j = 0; j < 4; ++j) {
+        bv[j] = n0 + 16 * j + lr < a.N;  // this lane's column
+        bp[j] = a.w + (size_t(g) * a.N + (bv[j] ? n0 + 16 * j + lr : 0u)) * a.K + lk;
+    }
 
     float4_t acc[4][4];
 #pragma unroll
@@ -110,7 +116,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) af[i] = av[i] ? load_frag(ap[i]) : zero;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bf[j] = load_frag(bp[j]);
+    for (int j = 0; j < 4; ++j) bf[j] = bv[j] ? load_frag(bp[j]) : zero;
     for (uint32_t k0 = 32; k0 <= a.K; k0 += 32) {
         half8_t an[4], bn[4];
         const bool more = k0 < a.K;
@@ -118,7 +124,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) an[i] = av[i] ? load_frag(ap[i] + k0) : zero;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) bn[j] = load_frag(bp[j] + k0);
+            for (int j = 0; j < 4; ++j) bn[j] = bv[j] ? load_frag(bp[j] + k0) : zero;
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -140,9 +146,10 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a) {
             if (p >= gend) continue;
             const uint32_t yrow = a.yr ? a.yr[p] : p;
             if (yrow >= a.n_slots) continue;
-            uint16_t *yp = a.y + size_t(yrow) * a.N + n0 + lr;
+            uint16_t *yp = a.y + size_t(yrow) * a.N + n0 + lr;  // only columns with bv[j] are stored
 #pragma unroll
-            for (int j = 0; j < 4; ++j) yp[16 * j] = uint16_t(float_to_half_bits(acc[i][j][r]));
+            for (int j = 0; j < 4; ++j)
+                if (bv[j]) yp[16 * j] = uint16_t(float_to_half_bits(acc[i][j][r]));
         }
     }
 }
@@ -154,7 +161,7 @@ extern "C" int iqk_grouped_gemm(int64_t in_features, int64_t out_features, int64
                                 const uint32_t *x_rows, const uint32_t *y_rows, void *y, void *stream) {
     using namespace iqk;
     if (in_features <= 0 || in_features % 32 || in_features > (int64_t(1) << 20)) return IQK_ERR_GEOMETRY;
-    if (out_features <= 0 || out_features % kGemmBN || out_features > (int64_t(1) << 20)) return IQK_ERR_GEOMETRY;
+    if (out_features <= 0 || out_features > (int64_t(1) << 20)) return IQK_ERR_GEOMETRY;
     if (n_groups < 0 || n_groups > (int64_t(1) << 20) || n_slots < 0 || n_slots > (int64_t(1) << 30))
         return IQK_ERR_ARGUMENT;
     if (n_x_rows < 0 || n_x_rows > 0xffffffffll) return IQK_ERR_ARGUMENT;
@@ -174,7 +181,7 @@ extern "C" int iqk_grouped_gemm(int64_t in_features, int64_t out_features, int64
     a.n_x_rows = uint32_t(n_x_rows);
     const uint64_t mtiles = (uint64_t(n_slots) + kGemmBM - 1) / kGemmBM + uint64_t(n_groups);
     if (mtiles > 0x7fffffffull) return IQK_ERR_ARGUMENT;
-    const dim3 grid{uint32_t(mtiles), uint32_t(out_features / kGemmBN)}, block{256};
+    const dim3 grid{uint32_t(mtiles), uint32_t((out_features + kGemmBN - 1) / kGemmBN)}, block{256};
     hipLaunchKernelGGL(grouped_gemm_kernel, grid, block, 0, as_stream(stream), a);
     return record_launch(hipGetLastError());
 }

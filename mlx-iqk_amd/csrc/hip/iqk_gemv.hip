@@ -36,6 +36,8 @@ struct GemvArgs {
     const uint32_t *x;  // f16 pairs
     const void *s0, *s1, *s2, *s3, *s4;
     const uint32_t *sel;
+    const uint32_t *toks;  // NULL: pair m reads x row m / pairs_per_row; else toks[m]
+    uint32_t n_x_rows;
     uint32_t pairs_per_row;
     uint32_t num_experts;
     uint32_t out_features;
@@ -135,8 +137,9 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvArgs a) {
     const uint32_t m = blockIdx.y;
     const uint32_t row0 = blockIdx.x * 16;
     const uint32_t e = a.sel[m];
+    const uint32_t tok = a.toks ? a.toks[m] : m / a.pairs_per_row;
     uint16_t *yrow = a.y + size_t(m) * a.out_features + row0;
-    if (e >= a.num_experts) {
+    if (e >= a.num_experts || tok >= a.n_x_rows) {
         if (lane < 16) yrow[lane] = kHalfNaN;
         return;
     }
@@ -147,7 +150,6 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvArgs a) {
         __syncthreads();
     }
 
-    const uint32_t tok = m / a.pairs_per_row;
     const uint32_t *xrow = a.x + size_t(tok) * (N / 2) + 32 * lc;
     const size_t rowbase = size_t(e) * a.out_features + row0 + rsub;
 
@@ -296,23 +298,33 @@ int launch_gemv(int64_t n, const GemvArgs &a, uint32_t mats, hipStream_t st) {
 
 // The int8-MFMA path (iqk_gemv_mfma.hip); -1 when it does not apply.
 int gemv_mfma_dispatch(bool floor, int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
-                       const void *const *streams, int n_streams, const uint32_t *sel, uint32_t pairs_per_row,
-                       uint32_t mats, void *y, hipStream_t st);
+                       int64_t n_x_rows, const void *const *streams, int n_streams, const uint32_t *sel,
+                       const uint32_t *toks, bool union_runs, uint32_t pairs_per_row, uint32_t mats, void *y,
+                       hipStream_t st);
 
+// All GEMV entry points.  toks NULL: pair m reads x row m / pairs_per_row
+// (n_x_rows = mats / pairs_per_row); else x row toks[m] < n_x_rows (a row
+// beyond is a NaN output row) and union_runs picks the one-read-per-run form
+// where the MFMA path serves (the VALU path computes the same rows pair by
+// pair).
 template <bool FLOOR>
-int gemv_entry(int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
-               const void *const *streams, int n_streams, const uint32_t *sel, uint32_t pairs_per_row,
-               uint32_t mats, void *y, void *stream) {
+int gemv_entry(int member, int64_t n, int64_t out, int64_t num_experts, const void *x, int64_t n_x_rows,
+               const void *const *streams, int n_streams, const uint32_t *sel, const uint32_t *toks,
+               bool union_runs, uint32_t pairs_per_row, uint32_t mats, void *y, void *stream) {
     const int g = iqk_check_gemv_geometry(member, n, out);
     if (g != IQK_OK) return g;
+    if (toks && member == IQK_MEMBER_IQ1_S_R4) return IQK_ERR_MEMBER;  // no sorted/union form
     if (!x || !sel || !y || !streams_ok(streams, n_streams, member)) return IQK_ERR_ARGUMENT;
     if (num_experts <= 0 || num_experts > 0xffffffffll || pairs_per_row == 0 || mats % pairs_per_row)
         return IQK_ERR_ARGUMENT;
+    if (n_x_rows < 0 || n_x_rows > 0xffffffffll) return IQK_ERR_ARGUMENT;
     if (mats == 0) return IQK_OK;
+    // a pair whose row is out of range reads row 0 (and writes NaN): x needs one
+    if (n_x_rows == 0) return IQK_ERR_ARGUMENT;
     if (mats > 65535u) return IQK_ERR_ARGUMENT;
     hipStream_t st = as_stream(stream);
-    const int r =
-        gemv_mfma_dispatch(FLOOR, member, n, out, num_experts, x, streams, n_streams, sel, pairs_per_row, mats, y, st);
+    const int r = gemv_mfma_dispatch(FLOOR, member, n, out, num_experts, x, n_x_rows, streams, n_streams, sel,
+                                     toks, union_runs, pairs_per_row, mats, y, st);
     if (r >= 0) return r;
     GemvArgs a;
     a.x = static_cast<const uint32_t *>(x);
@@ -320,6 +332,8 @@ int gemv_entry(int member, int64_t n, int64_t out, int64_t num_experts, const vo
     a.s3 = n_streams > 3 ? streams[3] : nullptr;
     a.s4 = n_streams > 4 ? streams[4] : nullptr;
     a.sel = sel;
+    a.toks = toks;
+    a.n_x_rows = uint32_t(n_x_rows);
     a.pairs_per_row = pairs_per_row;
     a.num_experts = uint32_t(num_experts);
     a.out_features = uint32_t(out);
@@ -345,15 +359,35 @@ int iqk_check_gemv_geometry(int member, int64_t n, int64_t out) {
 int iqk_gemv(int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
              const void *const *streams, int n_streams, const uint32_t *sel, uint32_t pairs_per_row,
              uint32_t mats, void *y, void *stream) {
-    return iqk::gemv_entry<false>(member, n, out, num_experts, x, streams, n_streams, sel, pairs_per_row,
-                                  mats, y, stream);
+    const int64_t rows = pairs_per_row ? mats / pairs_per_row : 0;
+    return iqk::gemv_entry<false>(member, n, out, num_experts, x, rows, streams, n_streams, sel, nullptr, false,
+                                  pairs_per_row, mats, y, stream);
 }
 
 int iqk_gemv_floor(int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
                    const void *const *streams, int n_streams, const uint32_t *sel, uint32_t pairs_per_row,
                    uint32_t mats, void *y, void *stream) {
-    return iqk::gemv_entry<true>(member, n, out, num_experts, x, streams, n_streams, sel, pairs_per_row,
-                                 mats, y, stream);
+    const int64_t rows = pairs_per_row ? mats / pairs_per_row : 0;
+    return iqk::gemv_entry<true>(member, n, out, num_experts, x, rows, streams, n_streams, sel, nullptr, false,
+                                 pairs_per_row, mats, y, stream);
+}
+
+int iqk_gemv_sorted(int member, int64_t n, int64_t out, int64_t num_experts, const void *x, int64_t n_x_rows,
+                    const void *const *streams, int n_streams, const uint32_t *sorted_ids, const uint32_t *toks,
+                    uint32_t mats, void *y, void *stream) {
+    if (member == IQK_MEMBER_IQ1_S_R4) return IQK_ERR_MEMBER;  // no sorted form
+    if (!toks && mats) return IQK_ERR_ARGUMENT;
+    return iqk::gemv_entry<false>(member, n, out, num_experts, x, n_x_rows, streams, n_streams, sorted_ids, toks,
+                                  false, 1u, mats, y, stream);
+}
+
+int iqk_gemv_union(int member, int64_t n, int64_t out, int64_t num_experts, const void *x, int64_t n_x_rows,
+                   const void *const *streams, int n_streams, const uint32_t *sorted_ids, const uint32_t *toks,
+                   uint32_t mats, void *y, void *stream) {
+    if (member == IQK_MEMBER_IQ1_S_R4) return IQK_ERR_MEMBER;  // no union form
+    if (!toks && mats) return IQK_ERR_ARGUMENT;
+    return iqk::gemv_entry<false>(member, n, out, num_experts, x, n_x_rows, streams, n_streams, sorted_ids, toks,
+                                  true, 1u, mats, y, stream);
 }
 
 }  // extern "C"

@@ -59,7 +59,10 @@ struct Gemv2Args {
     const uint32_t *x;
     const void *s0, *s1, *s2, *s3, *s4;
     const uint32_t *sel;
+    const uint32_t *toks;  // sorted/union modes: activation row of each pair
     uint32_t pairs_per_row;
+    uint32_t mats;
+    uint32_t n_x_rows;
     uint32_t num_experts;
     uint32_t out_features;
     uint16_t *y;
@@ -516,11 +519,21 @@ using LaneOf = std::conditional_t<MEMBER == IQ2_KS, LaneIq2ks<N>,
                                   std::conditional_t<MEMBER == IQ2_K, LaneIq2k<N>,
                                                      LaneIq1s<N, Gemv2Shape<MEMBER, N>::WK>>>;
 
+// How a launch maps pairs to activation rows and stream reads.
+enum GemvMode : int {
+    kPairs = 0,   // pair m reads x[m / pairs_per_row]; one workgroup per (tile, pair)
+    kSorted = 1,  // pair m reads x[toks[m]]; one workgroup per (tile, pair)
+    kUnion = 2,   // as kSorted, but a run of equal adjacent ids streams its
+                  // expert's rows once: the run's first pair does the run
+};
+
 // Six wavefronts per SIMD: three workgroups of eight (N = 4096) or six of
 // four (N = 2048) per CU, so a 1-token routed decode's 768 workgroups are
-// resident at once.
-template <int MEMBER, int N, bool FLOOR>
-__global__ __launch_bounds__((Gemv2Shape<MEMBER, N>::THREADS)) __attribute__((amdgpu_waves_per_eu(6)))
+// resident at once.  kUnion keeps each lane's expanded weights in registers
+// across its run (134-182 VGPRs): two or three wavefronts per SIMD, no spills.
+template <int MEMBER, int N, bool FLOOR, int MODE>
+__global__ __launch_bounds__((Gemv2Shape<MEMBER, N>::THREADS))
+__attribute__((amdgpu_waves_per_eu(MODE == kUnion ? 2 : 6)))
 void gemv_mfma_kernel(Gemv2Args a) {
     using S = Gemv2Shape<MEMBER, N>;
     constexpr int KS = S::KS;
@@ -530,20 +543,39 @@ void gemv_mfma_kernel(Gemv2Args a) {
     const int wave = tid >> 6, l = tid & 63;
     const int n = l & 15, g = l >> 4;
     const int kq = wave % KS, tile = wave / KS;
-    const uint32_t tok = blockIdx.z;
-    const uint32_t m = tok * a.pairs_per_row + blockIdx.y;
+    const uint32_t m0 = MODE == kPairs ? blockIdx.z * a.pairs_per_row + blockIdx.y : blockIdx.z;
     const uint32_t rowg = blockIdx.x * kGroupRows;
+
+    // The run of pairs this workgroup serves: one pair, or for kUnion every
+    // pair of a run of equal ids (workgroups of the run's other pairs exit).
+    uint32_t run = 1;
+    if constexpr (MODE == kUnion) {
+        const uint32_t e_first = a.sel[m0];
+        if (m0 > 0 && a.sel[m0 - 1] == e_first) return;  // uniform: not the run's first pair
+        while (m0 + run < a.mats && a.sel[m0 + run] == e_first) ++run;
+    }
+    // Activation row of pair m; a row beyond x reads row 0 and yields NaN.
+    const auto x_row = [&](uint32_t m) -> uint32_t {
+        return MODE == kPairs ? blockIdx.z : a.toks[m];
+    };
 
     // Activation (and IQ1_S_R4 grid) loads first: they do not wait for the
     // expert id, and vector loads retire in order, so staging them waits for
     // none of the stream bytes issued after them.
-    const uint32_t xo = tok * (2 * N) + 32 * (uint32_t(tid) >> 1);
     const bool stager = tid < S::UNITS;  // uniform per wavefront
-    uint4_t x0 = {0u, 0u, 0u, 0u}, x1 = {0u, 0u, 0u, 0u};
-    if (stager) {
-        x0 = load_u4(bytes(a.x) + xo);
-        x1 = load_u4(bytes(a.x) + (xo + 16));
-    }
+    const auto load_x = [&](uint32_t tok, uint4_t &x0, uint4_t &x1) {
+        const uint32_t xo = tok * (2 * N) + 32 * (uint32_t(tid) >> 1);
+        x0 = uint4_t{0u, 0u, 0u, 0u};
+        x1 = uint4_t{0u, 0u, 0u, 0u};
+        if (stager) {
+            x0 = load_u4(bytes(a.x) + xo);
+            x1 = load_u4(bytes(a.x) + (xo + 16));
+        }
+    };
+    uint32_t tok = x_row(m0);
+    bool x_ok = MODE == kPairs || tok < a.n_x_rows;
+    uint4_t x0, x1;
+    load_x(x_ok ? tok : 0u, x0, x1);
     constexpr bool IQ1 = MEMBER == IQ1_S_R4;
     constexpr int GRID_CHUNKS = IQ1 && !FLOOR ? IQK_IQ1S_GRID_SIZE / 2 / S::THREADS : 0;  // uint4 per thread
     uint4_t gridv[GRID_CHUNKS > 0 ? GRID_CHUNKS : 1];
@@ -557,93 +589,128 @@ void gemv_mfma_kernel(Gemv2Args a) {
     // An id beyond the stack reads expert 0 (in bounds) and writes NaN rows.
     // No early exit: a branch here would let the compiler sink the loads
     // above behind the wait for the id.
-    const uint32_t e_raw = a.sel[m];
+    const uint32_t e_raw = a.sel[m0];
     const bool valid = e_raw < a.num_experts;  // uniform per workgroup
     const uint32_t e = valid ? e_raw : 0u;
-    uint16_t *ygroup = a.y + size_t(m) * a.out_features + rowg;
     const uint32_t row = e * a.out_features + rowg + 16 * tile + n;
     LaneOf<MEMBER, N> lane;
     lane.load(a, row, kq, g);
 
-    float acc;
-    if constexpr (FLOOR) {
-        const uint32_t h = x0.x + 3u * x0.y + 5u * x0.z + 7u * x0.w + 11u * x1.x + 13u * x1.y + 17u * x1.z +
-                           19u * x1.w + lane.hash();
-        acc = float(h & 0xffu);
-    } else {
+    // One pair's contraction.  Outside kUnion it runs once, straight-line: a
+    // loop here, even of one trip, costs the pair kernels registers.
+    const auto contract = [&](uint32_t q) {
+        const uint32_t m = m0 + q;
+        if (q > 0) {  // kUnion: the run's next pair, same stream registers
+            tok = x_row(m);
+            x_ok = tok < a.n_x_rows;
+            load_x(x_ok ? tok : 0u, x0, x1);
+        }
+        float acc;
+        if constexpr (FLOOR) {
+            const uint32_t h = x0.x + 3u * x0.y + 5u * x0.z + 7u * x0.w + 11u * x1.x + 13u * x1.y + 17u * x1.z +
+                               19u * x1.w + lane.hash();
+            acc = float(h & 0xffu);
+        } else {
+            if (q == 0) {
 #pragma unroll
-        for (int i = 0; i < GRID_CHUNKS; ++i) reinterpret_cast<uint4_t *>(sm.b8)[tid + i * S::THREADS] = gridv[i];
-        if (KTAB && tid < 32) sm.ktab[tid] = ktv;
-        if (stager)
-            stage_activations<N, !IQ1, !kMaskedA<MEMBER>, kExpBlock<MEMBER>, S::WK>(
-                sm.dig, sm.sbs, IQ1 ? sm.fsum : nullptr, MEMBER == IQ2_K ? sm.fw : nullptr, tid, x0, x1);
+                for (int i = 0; i < GRID_CHUNKS; ++i)
+                    reinterpret_cast<uint4_t *>(sm.b8)[tid + i * S::THREADS] = gridv[i];
+                if (KTAB && tid < 32) sm.ktab[tid] = ktv;
+            }
+            if (stager)
+                stage_activations<N, !IQ1, !kMaskedA<MEMBER>, kExpBlock<MEMBER>, S::WK>(
+                    sm.dig, sm.sbs, IQ1 ? sm.fsum : nullptr, MEMBER == IQ2_K ? sm.fw : nullptr, tid, x0, x1);
+            __syncthreads();
+            const int ai = l & 15;  // this lane's A row
+            const bool data = (ai >> 2) == g && (ai & 3) < 3;
+            constexpr int LANE_K = IQ1 ? 128 : 64;
+            const uint8_t *abase =
+                sm.dig + (data || kMaskedA<MEMBER> ? (ai & 3) * kPlaneStride<N> + S::WK * kq + LANE_K * g
+                                                   : 3 * kPlaneStride<N>);
+            const float *sbs = sm.sbs + (S::WK / 32) * kq;
+            if constexpr (IQ1)
+                acc = lane.decode(abase, data, sbs, sm.fsum + (S::WK / 32) * kq, sm.b8, g);
+            else if constexpr (MEMBER == IQ2_KS)
+                acc = lane.decode(abase, data, sbs, g);
+            else
+                acc = lane.decode(abase, sm.sbs + (S::WK / 64) * kq, sm.fw + (S::WK / 16) * kq, sm.ktab, g);
+        }
+        // Partials of the row's lanes and wavefronts: wave 0 sums them after
+        // the barrier; the next pair's staging and partials come only after
+        // its own barrier, which wave 0 reaches after summing.
+        sm.part[kq][g][16 * tile + n] = acc;
         __syncthreads();
-        const int ai = l & 15;  // this lane's A row
-        const bool data = (ai >> 2) == g && (ai & 3) < 3;
-        constexpr int LANE_K = IQ1 ? 128 : 64;
-        const uint8_t *abase = sm.dig + (data || kMaskedA<MEMBER> ? (ai & 3) * kPlaneStride<N> + S::WK * kq + LANE_K * g
-                                                                 : 3 * kPlaneStride<N>);
-        const float *sbs = sm.sbs + (S::WK / 32) * kq;
-        if constexpr (IQ1)
-            acc = lane.decode(abase, data, sbs, sm.fsum + (S::WK / 32) * kq, sm.b8, g);
-        else if constexpr (MEMBER == IQ2_KS)
-            acc = lane.decode(abase, data, sbs, g);
-        else
-            acc = lane.decode(abase, sm.sbs + (S::WK / 64) * kq, sm.fw + (S::WK / 16) * kq, sm.ktab, g);
-    }
-    sm.part[kq][g][16 * tile + n] = acc;
-    __syncthreads();
-    if (tid < kGroupRows) {
-        float sum = 0.f;
+        if (tid < kGroupRows) {
+            float sum = 0.f;
 #pragma unroll
-        for (int k = 0; k < KS; ++k) sum += (sm.part[k][0][tid] + sm.part[k][1][tid]) + (sm.part[k][2][tid] + sm.part[k][3][tid]);
-        ygroup[tid] = valid ? uint16_t(float_to_half_bits(sum)) : kHalfNaN;
+            for (int k = 0; k < KS; ++k)
+                sum += (sm.part[k][0][tid] + sm.part[k][1][tid]) + (sm.part[k][2][tid] + sm.part[k][3][tid]);
+            a.y[size_t(m) * a.out_features + rowg + tid] = valid && x_ok ? uint16_t(float_to_half_bits(sum)) : kHalfNaN;
+        }
+    };
+    if constexpr (MODE == kUnion) {
+        for (uint32_t q = 0; q < run; ++q) contract(q);
+    } else {
+        contract(0);
     }
 }
 
-template <int MEMBER, bool FLOOR>
+template <int MEMBER, bool FLOOR, int MODE>
 int launch_gemv_mfma(int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t st) {
-    const dim3 grid{a.out_features / kGroupRows, a.pairs_per_row, mats / a.pairs_per_row};
+    const dim3 grid = MODE == kPairs ? dim3{a.out_features / kGroupRows, a.pairs_per_row, mats / a.pairs_per_row}
+                                     : dim3{a.out_features / kGroupRows, 1u, mats};
     const dim3 block4096{uint32_t(Gemv2Shape<MEMBER, 4096>::THREADS)}, block2048{uint32_t(Gemv2Shape<MEMBER, 2048>::THREADS)};
     if (n == 4096)
-        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 4096, FLOOR>), grid, block4096, 0, st, a);
+        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 4096, FLOOR, MODE>), grid, block4096, 0, st, a);
     else
-        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 2048, FLOOR>), grid, block2048, 0, st, a);
+        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 2048, FLOOR, MODE>), grid, block2048, 0, st, a);
     return record_launch(hipGetLastError());
 }
 
-template <bool FLOOR>
+template <bool FLOOR, int MODE>
 int launch_member(int member, int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t st) {
     switch (member) {
-        case IQK_MEMBER_IQ2_KS: return launch_gemv_mfma<IQ2_KS, FLOOR>(n, a, mats, st);
-        case IQK_MEMBER_IQ2_K: return launch_gemv_mfma<IQ2_K, FLOOR>(n, a, mats, st);
-        default: return launch_gemv_mfma<IQ1_S_R4, FLOOR>(n, a, mats, st);
+        case IQK_MEMBER_IQ2_KS: return launch_gemv_mfma<IQ2_KS, FLOOR, MODE>(n, a, mats, st);
+        case IQK_MEMBER_IQ2_K: return launch_gemv_mfma<IQ2_K, FLOOR, MODE>(n, a, mats, st);
+        default:
+            if constexpr (MODE == kPairs) return launch_gemv_mfma<IQ1_S_R4, FLOOR, MODE>(n, a, mats, st);
+            return IQK_ERR_MEMBER;  // no sorted or union form for IQ1_S_R4
     }
 }
 
 // Called by the GEMV entry points (after their argument checks) when
 // out_features is a multiple of the workgroup's 32 rows; returns -1 when this
-// path does not apply.
+// path does not apply.  `toks` NULL = pairs mode (x row m / pairs_per_row);
+// else x row toks[m] of n_x_rows, and `union_runs` selects the one-read-per-
+// run form.
 int gemv_mfma_dispatch(bool floor, int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
-                       const void *const *streams, int n_streams, const uint32_t *sel, uint32_t pairs_per_row,
-                       uint32_t mats, void *y, hipStream_t st) {
+                       int64_t n_x_rows, const void *const *streams, int n_streams, const uint32_t *sel,
+                       const uint32_t *toks, bool union_runs, uint32_t pairs_per_row, uint32_t mats, void *y,
+                       hipStream_t st) {
     if (out % kGroupRows) return -1;
     // 32-bit offsets: every stream (the code plane is the largest, N/4 bytes a
     // row) and the activations stay below 4 GiB
     const uint64_t lim = uint64_t(1) << 32;
     if (uint64_t(num_experts) * uint64_t(out) * uint64_t(n / 4) >= lim) return -1;
-    if (uint64_t(mats / pairs_per_row) * uint64_t(2 * n) >= lim) return -1;
+    if (uint64_t(n_x_rows) * uint64_t(2 * n) >= lim) return -1;
     Gemv2Args a;
     a.x = static_cast<const uint32_t *>(x);
     a.s0 = streams[0]; a.s1 = streams[1]; a.s2 = streams[2];
     a.s3 = n_streams > 3 ? streams[3] : nullptr;
     a.s4 = n_streams > 4 ? streams[4] : nullptr;
     a.sel = sel;
+    a.toks = toks;
     a.pairs_per_row = pairs_per_row;
+    a.mats = mats;
+    a.n_x_rows = uint32_t(n_x_rows);
     a.num_experts = uint32_t(num_experts);
     a.out_features = uint32_t(out);
     a.y = static_cast<uint16_t *>(y);
-    return floor ? launch_member<true>(member, n, a, mats, st) : launch_member<false>(member, n, a, mats, st);
+    if (!toks)
+        return floor ? launch_member<true, kPairs>(member, n, a, mats, st) : launch_member<false, kPairs>(member, n, a, mats, st);
+    if (floor) return IQK_ERR_ARGUMENT;
+    return union_runs ? launch_member<false, kUnion>(member, n, a, mats, st)
+                      : launch_member<false, kSorted>(member, n, a, mats, st);
 }
 
 }  // namespace iqk

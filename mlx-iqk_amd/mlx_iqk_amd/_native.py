@@ -12,7 +12,7 @@ from pathlib import Path
 
 from .build import HIP_LIB
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK, ERR_MEMBER, ERR_GEOMETRY, ERR_ARGUMENT, ERR_LAUNCH = 0, 1, 2, 3, 4
 _CODES = {ERR_MEMBER: "unknown member", ERR_GEOMETRY: "unsized geometry",
@@ -33,8 +33,14 @@ SIGNATURES = {
                          c_void_p, c_uint32, c_uint32, c_void_p, c_void_p]),
     "iqk_gemv_floor": (c_int, [c_int, c_int64, c_int64, c_int64, c_void_p, ctypes.POINTER(c_void_p), c_int,
                                c_void_p, c_uint32, c_uint32, c_void_p, c_void_p]),
+    "iqk_gemv_sorted": (c_int, [c_int, c_int64, c_int64, c_int64, c_void_p, c_int64, ctypes.POINTER(c_void_p),
+                                c_int, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p]),
+    "iqk_gemv_union": (c_int, [c_int, c_int64, c_int64, c_int64, c_void_p, c_int64, ctypes.POINTER(c_void_p),
+                               c_int, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p]),
     "iqk_dequant": (c_int, [c_int, c_int64, c_int64, c_int64, ctypes.POINTER(c_void_p), c_int,
                             c_void_p, c_int64, c_void_p, c_void_p]),
+    "iqk_dequant_rows": (c_int, [c_int, c_int64, c_int64, c_int64, ctypes.POINTER(c_void_p), c_int,
+                                 c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
     "iqk_dequant_floor": (c_int, [c_int, c_int64, c_int64, c_int64, ctypes.POINTER(c_void_p), c_int,
                                   c_void_p, c_int64, c_void_p, c_void_p]),
     "iqk_grouped_gemm": (c_int, [c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p,

@@ -28,8 +28,6 @@ WEIGHTS_PER_LANE = 64
 SUPPORTED_IN_FEATURES = (2048, 4096)
 DEQUANT_THREADS = 256
 TABLE_INPUT_NAMES = {"iq2_ks": "vtab", "iq2_k": "vtab", "iq1_s_r4": "grid"}
-GROUPED_GEMM_N_TILE = 256
-"""out_features granularity of the grouped GEMM."""
 
 
 class IqkKernelError(RuntimeError):
@@ -152,16 +150,80 @@ def gemv(member: str, x: torch.Tensor, streams: list[torch.Tensor], sel: torch.T
     return out
 
 
+def check_iq2_member(member: str) -> str:
+    """Members the sorted and union GEMVs cover (reference: src/mlx_iqk/kernels.py:89-97)."""
+    check_member(member)
+    if member not in IQ2_MEMBERS:
+        raise IqkKernelError(
+            f"the sorted and union decode GEMVs cover {IQ2_MEMBERS}; {member!r} has no such variant")
+    return member
+
+
+def gemv_sorted(member: str, x: torch.Tensor, streams: list[torch.Tensor], sorted_ids: torch.Tensor,
+                toks: torch.Tensor, num_experts: int, out_features: int, *, union: bool = False,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode GEMV over expert-sorted pairs: ``y[p] = W[sorted_ids[p]] @ x[toks[p]]``.
+
+    fp16 ``[mats, out]``; each element equals :func:`gemv`'s for the same
+    (expert, activation row), bit for bit.  ``union=True`` streams each run of
+    equal adjacent ids once (the multi-token verify shape,
+    src/mlx_iqk/kernels.py:484-578); otherwise one workgroup per pair
+    (src/mlx_iqk/kernels.py:404-482).  IQ2 members only.
+    """
+    check_iq2_member(member)
+    n = int(x.shape[-1])
+    check_gemv_geometry(n, out_features)
+    device = check_streams(member, streams, num_experts, out_features, n)
+    _require_cuda(x, "x", torch.float16, device)
+    _require_cuda(sorted_ids, "sorted_ids", (torch.int32, torch.uint32), device)
+    _require_cuda(toks, "toks", (torch.int32, torch.uint32), device)
+    if x.dim() != 2 or sorted_ids.dim() != 1 or toks.dim() != 1:
+        raise IqkKernelError("x must be [rows, in_features], sorted_ids and toks [mats]")
+    mats = int(sorted_ids.numel())
+    if int(toks.numel()) != mats:
+        raise IqkKernelError(f"toks carries {int(toks.numel())} rows for {mats} pairs")
+    if out is None:
+        out = torch.empty((mats, out_features), dtype=torch.float16, device=device)
+    else:
+        _require_cuda(out, "out", torch.float16, device)
+        if tuple(out.shape) != (mats, out_features):
+            raise IqkKernelError(f"out must be {(mats, out_features)}, got {tuple(out.shape)}")
+    if mats == 0:
+        return out
+    lib = _native.load()
+    fn = lib.iqk_gemv_union if union else lib.iqk_gemv_sorted
+    ptrs = _native.pointer_array([t.data_ptr() for t in streams])
+    stream = _stream_ptr(device)
+    # The pair index rides gridDim.z: chunks of at most 65535 pairs.  A run of
+    # equal ids split by a chunk boundary is read once per chunk.
+    for m0 in range(0, mats, 65535):
+        cnt = min(65535, mats - m0)
+        rc = fn(_native.MEMBER_IDS[member], n, out_features, num_experts, x.data_ptr(), int(x.shape[0]), ptrs,
+                len(streams), sorted_ids.data_ptr() + 4 * m0, toks.data_ptr() + 4 * m0, cnt,
+                out.data_ptr() + m0 * out_features * 2, stream)
+        _native.check(rc, f"iqk_gemv_{'union' if union else 'sorted'}({member}, {n}x{out_features})")
+    return out
+
+
 def dequant(member: str, streams: list[torch.Tensor], num_experts: int, out_features: int, in_features: int,
             *, slot_of_expert: torch.Tensor | None = None, n_slots: int | None = None, floor: bool = False,
-            out: torch.Tensor | None = None) -> torch.Tensor:
-    """Producer: fp16 ``[n_slots, out, in]``, slot ``slot_of_expert[e]`` <- expert ``e``.
+            row_start: int = 0, rows: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Producer: fp16 ``[n_slots, rows, in]``, slot ``slot_of_expert[e]`` <- rows
+    ``[row_start, row_start + rows)`` of expert ``e`` (default: every row).
 
     Without ``slot_of_expert`` every expert lands in its own slot.  Slots no
-    expert maps to are left unwritten.
+    expert maps to are left unwritten.  A row range is bit-identical to the
+    same slice of the full reconstruction.
     """
     check_member(member)
     check_dequant_geometry(in_features, out_features)
+    row_start = int(row_start)
+    rows = out_features - row_start if rows is None else int(rows)
+    ranged = row_start != 0 or rows != out_features
+    if row_start < 0 or rows <= 0 or row_start + rows > out_features:
+        raise IqkKernelError(f"row range [{row_start}, {row_start + rows}) is outside out_features {out_features}")
+    if floor and (row_start or rows != out_features):
+        raise IqkKernelError("the producer's floor covers full experts only")
     device = check_streams(member, streams, num_experts, out_features, in_features)
     if slot_of_expert is None:
         n_slots = num_experts if n_slots is None else int(n_slots)
@@ -175,7 +237,7 @@ def dequant(member: str, streams: list[torch.Tensor], num_experts: int, out_feat
         if n_slots is None:
             raise IqkKernelError("n_slots is required with slot_of_expert")
         slot_ptr = slot_of_expert.data_ptr()
-    shape = (int(n_slots), out_features, in_features)
+    shape = (int(n_slots), rows, in_features)
     if out is None:
         out = torch.empty(shape, dtype=torch.float16, device=device)
     else:
@@ -183,9 +245,15 @@ def dequant(member: str, streams: list[torch.Tensor], num_experts: int, out_feat
         if tuple(out.shape) != shape:
             raise IqkKernelError(f"out must be {shape}, got {tuple(out.shape)}")
     lib = _native.load()
-    fn = lib.iqk_dequant_floor if floor else lib.iqk_dequant
     ptrs = _native.pointer_array([t.data_ptr() for t in streams])
-    rc = fn(_native.MEMBER_IDS[member], in_features, out_features, num_experts, ptrs, len(streams),
+    mid = _native.MEMBER_IDS[member]
+    if ranged:
+        rc = lib.iqk_dequant_rows(mid, in_features, out_features, num_experts, ptrs, len(streams), row_start,
+                                  rows, slot_ptr, int(n_slots), out.data_ptr(), _stream_ptr(device))
+        _native.check(rc, f"iqk_dequant_rows({member}, {in_features}x{out_features}, [{row_start}, +{rows}))")
+        return out
+    fn = lib.iqk_dequant_floor if floor else lib.iqk_dequant
+    rc = fn(mid, in_features, out_features, num_experts, ptrs, len(streams),
             slot_ptr, int(n_slots), out.data_ptr(), _stream_ptr(device))
     _native.check(rc, f"iqk_dequant{'_floor' if floor else ''}({member}, {in_features}x{out_features})")
     return out
@@ -210,8 +278,8 @@ def grouped_gemm(x: torch.Tensor, w: torch.Tensor, group_offsets: torch.Tensor, 
     P = int(x_rows.numel())
     if tuple(group_offsets.shape) != (G + 1,):
         raise IqkKernelError(f"group_offsets must be [{G + 1}]")
-    if N % GROUPED_GEMM_N_TILE or K % 32:
-        raise IqkKernelError(f"grouped gemm needs N % {GROUPED_GEMM_N_TILE} == 0 and K % 32 == 0")
+    if N <= 0 or K % 32:
+        raise IqkKernelError(f"grouped gemm needs N > 0 and K % 32 == 0, got N={N}, K={K}")
     if y_rows is not None:
         _require_cuda(y_rows, "y_rows", (torch.int32, torch.uint32), device)
         if y_rows.numel() != P:
@@ -230,8 +298,8 @@ def grouped_gemm(x: torch.Tensor, w: torch.Tensor, group_offsets: torch.Tensor, 
 
 
 __all__ = [
-    "DEQUANT_THREADS", "GROUPED_GEMM_N_TILE", "IQ2_MEMBERS", "MEMBERS", "ROWS_PER_TG",
+    "DEQUANT_THREADS", "IQ2_MEMBERS", "MEMBERS", "ROWS_PER_TG",
     "SUPPORTED_IN_FEATURES", "TABLE_INPUT_NAMES", "WEIGHTS_PER_LANE", "IqkKernelError",
     "check_dequant_geometry", "check_gemv_geometry", "check_streams", "dequant", "dequant_input_names",
-    "gemv", "gemv_input_names", "grouped_gemm", "stream_dtypes",
+    "check_iq2_member", "gemv", "gemv_input_names", "gemv_sorted", "grouped_gemm", "stream_dtypes",
 ]

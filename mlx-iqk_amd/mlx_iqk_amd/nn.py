@@ -140,6 +140,23 @@ class IqkSwitchLinear(torch.nn.Module):
         return kernels.dequant(self.member, self._streams(), self.num_experts, self.out_features,
                                self.in_features, slot_of_expert=slot_of_expert, n_slots=n_slots)
 
+    def dequantized_range(self, start: int, rows: int) -> torch.Tensor:
+        """fp16 dequantization of out rows ``[start, start + rows)`` of every
+        expert, ``[E, rows, in]``: bit-identical to the same slice of
+        :meth:`dequantized` (reference: src/mlx_iqk/nn.py:171-201).  Range-sized
+        buffers bound the fp16 memory a sorted prefill holds at once."""
+        start, rows = int(start), int(rows)
+        self._check_range(start, rows)
+        return kernels.dequant(self.member, self._streams(), self.num_experts, self.out_features,
+                               self.in_features, row_start=start, rows=rows)
+
+    def _check_range(self, start: int, rows: int) -> None:
+        if rows <= 0 or rows & (rows - 1):
+            raise IqkRuntimeError(f"range rows {rows} is not a positive power of two")
+        if start < 0 or start + rows > self.out_features:
+            raise IqkRuntimeError(
+                f"range [{start}, {start + rows}) is outside out_features {self.out_features}")
+
     # -- call -------------------------------------------------------------------
 
     def forward(self, x: torch.Tensor, indices: torch.Tensor, sorted_indices: bool = False) -> torch.Tensor:
@@ -163,6 +180,37 @@ class IqkSwitchLinear(torch.nn.Module):
                            self.out_features)
         return out.reshape(list(indices.shape) + [self.out_features]).unsqueeze(-2)
 
+    def gemv_sorted(self, x: torch.Tensor, sorted_ids: torch.Tensor, toks: torch.Tensor) -> torch.Tensor:
+        """Fused GEMV over expert-sorted pairs, one workgroup per pair
+        (reference: src/mlx_iqk/nn.py:273-299).
+
+        Row ``p`` is ``x[toks[p]]`` through expert ``sorted_ids[p]``, each
+        element bit-identical to :meth:`gemv`'s for the same pair, so the
+        result is the pair GEMV's rows in the caller's sorted order.  IQ2
+        members only.
+        """
+        xt, sel, tok = self._sorted_operands(x, sorted_ids, toks)
+        return kernels.gemv_sorted(self.member, xt, self._streams(), sel, tok, self.num_experts,
+                                   self.out_features)
+
+    def gemv_union(self, x: torch.Tensor, sorted_ids: torch.Tensor, toks: torch.Tensor) -> torch.Tensor:
+        """:meth:`gemv_sorted` reading each distinct expert once per run of
+        equal adjacent ids: the multi-token verify shape, where several pairs
+        select one expert (reference: src/mlx_iqk/nn.py:301-333).  Output and
+        arithmetic identical to :meth:`gemv_sorted`; the caller applies the
+        inverse permutation."""
+        xt, sel, tok = self._sorted_operands(x, sorted_ids, toks)
+        return kernels.gemv_sorted(self.member, xt, self._streams(), sel, tok, self.num_experts,
+                                   self.out_features, union=True)
+
+    def _sorted_operands(self, x, sorted_ids, toks):
+        xt = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
+        sel = sorted_ids.reshape(-1).to(torch.int32).contiguous()
+        tok = toks.reshape(-1).to(device=sel.device, dtype=torch.int32).contiguous()
+        if tok.numel() != sel.numel():
+            raise IqkRuntimeError(f"toks carries {tok.numel()} rows for {sel.numel()} pairs")
+        return xt, sel, tok
+
     def prefill(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         """Producer + sorted grouped GEMM; the dequantized route of ``forward``.
 
@@ -170,6 +218,18 @@ class IqkSwitchLinear(torch.nn.Module):
         batch shape is ``broadcast(x.shape[:-2], indices.shape)`` and each pair
         contracts its ``x.shape[-2]`` rows.
         """
+        return self._sorted_matmul(x, indices, 0, self.out_features)
+
+    def sorted_matmul_range(self, x: torch.Tensor, indices: torch.Tensor, start: int, rows: int) -> torch.Tensor:
+        """The sorted dequantized projection over out rows ``[start, start + rows)``
+        (reference: src/mlx_iqk/nn.py:203-219): ``[..., M, rows]``.
+        Concatenating the ranges along the last axis reproduces
+        :meth:`prefill`, element for element (each is the same dot product)."""
+        start, rows = int(start), int(rows)
+        self._check_range(start, rows)
+        return self._sorted_matmul(x, indices, start, rows)
+
+    def _sorted_matmul(self, x: torch.Tensor, indices: torch.Tensor, start: int, rows: int) -> torch.Tensor:
         if x.shape[-1] != self.in_features or x.dim() < 2:
             raise IqkRuntimeError(f"x must be [..., M, {self.in_features}], got {tuple(x.shape)}")
         device = self.qs.device
@@ -178,7 +238,7 @@ class IqkSwitchLinear(torch.nn.Module):
         batch = torch.broadcast_shapes(tuple(xb.shape[:-2]), tuple(indices.shape))
         P = math.prod(batch)
         if P == 0:
-            return torch.empty(tuple(batch) + (M, self.out_features), dtype=torch.float16, device=device)
+            return torch.empty(tuple(batch) + (M, rows), dtype=torch.float16, device=device)
         xbatch = tuple(xb.shape[:-2])
         xflat = xb.reshape(-1, self.in_features).contiguous()
         xidx = torch.arange(math.prod(xbatch), device=device).reshape(xbatch).broadcast_to(batch).reshape(-1)
@@ -199,9 +259,10 @@ class IqkSwitchLinear(torch.nn.Module):
         r = torch.arange(M, device=device)
         x_rows = (xidx[order][:, None] * M + r).reshape(-1).to(torch.int32)
         y_rows = (order[:, None] * M + r).reshape(-1).to(torch.int32)
-        w = self.dequantized_experts(slot_of_expert, n_slots)
+        w = kernels.dequant(self.member, self._streams(), E, self.out_features, self.in_features,
+                            slot_of_expert=slot_of_expert, n_slots=n_slots, row_start=start, rows=rows)
         y = kernels.grouped_gemm(xflat, w, offsets, x_rows, y_rows)
-        return y.reshape(tuple(batch) + (M, self.out_features))
+        return y.reshape(tuple(batch) + (M, rows))
 
 
 __all__ = ["DECODE_MAT_LIMIT", "IqkKernelError", "IqkRuntimeError", "IqkSwitchLinear", "grid_table",

@@ -77,7 +77,8 @@ def test_entry_points_refuse_bad_arguments_before_launching(lib):
     assert lib.iqk_dequant(2, 2048, 32, 4, streams, 5, None, 4, p, None) == _native.ERR_ARGUMENT
     assert lib.iqk_dequant(2, 2048, 32, 4, streams, 3, None, 2, p, None) == _native.ERR_ARGUMENT
     assert lib.iqk_dequant_floor(0, 2048, 32, 0, streams, 5, None, 4, p, None) == _native.ERR_ARGUMENT
-    assert lib.iqk_grouped_gemm(4096, 2000, 4, 8, p, 8, p, p, p, None, p, None) == _native.ERR_GEOMETRY
+    assert lib.iqk_grouped_gemm(4080, 2048, 4, 8, p, 8, p, p, p, None, p, None) == _native.ERR_GEOMETRY
+    assert lib.iqk_grouped_gemm(4096, 0, 4, 8, p, 8, p, p, p, None, p, None) == _native.ERR_GEOMETRY
     assert lib.iqk_grouped_gemm(4020, 2048, 4, 8, p, 8, p, p, p, None, p, None) == _native.ERR_GEOMETRY
     assert lib.iqk_grouped_gemm(4096, 2048, 4, 8, None, 8, p, p, p, None, p, None) == _native.ERR_ARGUMENT
     # empty work is a no-op success, with no launch
@@ -91,3 +92,23 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_native, "library_path", lambda: tmp_path / "absent.so")
     with pytest.raises(_native.IqkNativeError):
         _native.load()
+
+
+def test_sorted_union_and_range_entry_points_refuse_bad_arguments(lib):
+    p = ctypes.c_void_p(16)  # never dereferenced: every call below is refused first
+    streams = _native.pointer_array([16] * 5)
+    for fn in (lib.iqk_gemv_sorted, lib.iqk_gemv_union):
+        # IQ1_S_R4 has no sorted or union form (reference: _check_iq2_member)
+        assert fn(2, 4096, 2048, 256, p, 2, streams, 3, p, p, 6, p, None) == _native.ERR_MEMBER
+        assert fn(2, 4096, 2048, 256, p, 2, streams, 3, p, p, 0, p, None) == _native.ERR_MEMBER
+        # pairs without a token map, negative row count, unsized out
+        assert fn(0, 4096, 2048, 256, p, 2, streams, 5, p, None, 6, p, None) == _native.ERR_ARGUMENT
+        assert fn(0, 4096, 2048, 256, p, -1, streams, 5, p, p, 6, p, None) == _native.ERR_ARGUMENT
+        assert fn(0, 4096, 2048, 256, p, 0, streams, 5, p, p, 6, p, None) == _native.ERR_ARGUMENT
+        assert fn(1, 4096, 2040, 256, p, 2, streams, 4, p, p, 6, p, None) == _native.ERR_GEOMETRY
+        assert fn(0, 4096, 2048, 256, p, 2, streams, 5, p, p, 0, p, None) == _native.OK  # nothing to do
+    # ranges outside [0, out_features) or empty
+    for start, rows in ((16, 32), (-1, 8), (0, 0), (0, 33), (31, 2)):
+        assert lib.iqk_dequant_rows(0, 2048, 32, 4, streams, 5, start, rows, None, 4, p, None) == _native.ERR_GEOMETRY
+    assert lib.iqk_dequant_rows(0, 2048, 32, 4, streams, 5, 0, 32, None, 3, p, None) == _native.ERR_ARGUMENT
+    assert lib.iqk_dequant_rows(0, 2048, 32, 4, streams, 5, 0, 32, p, 0, p, None) == _native.OK

@@ -232,7 +232,7 @@ def test_floor_kernels_run(device, member, n):
 # -- the grouped GEMM -----------------------------------------------------------------
 
 
-@pytest.mark.parametrize("K,N", [(4096, 2048), (2048, 4096), (2048, 256)])
+@pytest.mark.parametrize("K,N", [(4096, 2048), (2048, 4096), (2048, 256), (2048, 32), (4096, 272)])
 def test_grouped_gemm_matches_a_float64_reference(device, K, N):
     print(f"grouped gemm K={K} N={N}", flush=True)
     rng = np.random.default_rng(K + N)

@@ -15,7 +15,8 @@ import torch
 import wirepack
 from mlx_iqk_amd import format as fmt
 from mlx_iqk_amd.iq1grid import grid_values
-from mlx_iqk_amd.nn import DECODE_MAT_LIMIT, IqkRuntimeError, IqkSwitchLinear, grid_table, member_table, value_table
+from mlx_iqk_amd.nn import (DECODE_MAT_LIMIT, IqkKernelError, IqkRuntimeError, IqkSwitchLinear, grid_table,
+                             member_table, value_table)
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -202,3 +203,202 @@ def test_routed_geometry_at_full_size(device):
         w = oracle.dequantize(member, wire[e * out + rows], n).astype(np.float64)
         want = w @ x[0, 0, 0].astype(np.float64)
         assert np.max(np.abs(got[k, rows] - want)) / np.max(np.abs(want)) < 1.5e-3, e
+
+
+# -- sorted and union GEMVs (reference: tests/test_nn.py:180-295) ------------
+
+IQ2 = ("iq2_ks", "iq2_k")
+
+
+def _union_operands(idx, top_k, device):
+    """Pairs sorted by expert: the sorted ids, each pair's token row, the
+    order and its inverse."""
+    flat = torch.from_numpy(np.ascontiguousarray(idx).reshape(-1).astype(np.int64)).to(device)
+    order = torch.argsort(flat, stable=True)
+    sorted_ids = flat[order].to(torch.int32)
+    toks = (order // top_k).to(torch.int32)
+    inv = torch.argsort(order)
+    return sorted_ids, toks, order, inv
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy()
+
+
+@pytest.mark.parametrize("member", IQ2)
+@pytest.mark.parametrize("n", (2048, 4096))
+@pytest.mark.parametrize("out", (OUT, 48))
+def test_union_gemv_is_bit_identical_to_the_pair_gemv(device, member, n, out):
+    """Duplicate-heavy selection: runs start at pair 0 and end at the last
+    pair.  out=48 is not a multiple of the 32-row MFMA workgroup, so the
+    VALU GEMV serves it."""
+    print(f"union gemv {member} n={n} out={out}", flush=True)
+    module, _ = _module(member, n, wirepack.seed_for(member, n, "union"), device, out=out)
+    rng = np.random.default_rng(71)
+    tokens, top_k = 6, 6
+    idx = rng.integers(0, 5, size=(tokens, top_k)).astype(np.int32)
+    x = torch.from_numpy(rng.standard_normal((tokens, 1, 1, n)).astype(np.float16)).to(device)
+    pair = module.gemv(x, torch.from_numpy(idx).to(device))
+    sorted_ids, toks, _order, inv = _union_operands(idx, top_k, device)
+    got = module.gemv_union(x, sorted_ids, toks)
+    assert tuple(got.shape) == (tokens * top_k, out)
+    assert np.array_equal(_bits(got[inv].reshape(pair.shape)), _bits(pair))
+
+
+@pytest.mark.parametrize("member", IQ2)
+@pytest.mark.parametrize("n", (2048, 4096))
+def test_union_gemv_serves_the_down_operand_shape(device, member, n):
+    """One activation row per pair: toks is the sort order itself."""
+    module, ref = _module(member, n, wirepack.seed_for(member, n, "union_down"), device)
+    rng = np.random.default_rng(73)
+    tokens, top_k = 6, 6
+    idx = rng.integers(0, 5, size=(tokens, top_k)).astype(np.int32)
+    xn = rng.standard_normal((tokens, top_k, 1, n)).astype(np.float16)
+    x = torch.from_numpy(xn).to(device)
+    pair = module.gemv(x, torch.from_numpy(idx).to(device))
+    sorted_ids, _toks, order, inv = _union_operands(idx, top_k, device)
+    got = module.gemv_union(x, sorted_ids, order.to(torch.int32))[inv].reshape(pair.shape)
+    assert np.array_equal(_bits(got), _bits(pair))
+    want = np.stack([[ref[idx[t, k]].astype(np.float64) @ xn[t, k, 0].astype(np.float64)
+                      for k in range(top_k)] for t in range(tokens)])[:, :, None, :]
+    assert _rel(got, want) < 1.5e-3
+
+
+@pytest.mark.parametrize("member", IQ2)
+def test_union_gemv_covers_the_run_extremes(device, member):
+    """A single all-pairs run and an all-distinct selection both serve."""
+    n = 2048
+    module, _ = _module(member, n, 79, device)
+    rng = np.random.default_rng(83)
+    tokens, top_k = 4, 2
+    x = torch.from_numpy(rng.standard_normal((tokens, 1, 1, n)).astype(np.float16)).to(device)
+    for idx in (np.full((tokens, top_k), 3, dtype=np.int32),
+                np.arange(tokens * top_k, dtype=np.int32).reshape(tokens, top_k)):
+        pair = module.gemv(x, torch.from_numpy(idx).to(device))
+        sorted_ids, toks, _order, inv = _union_operands(idx, top_k, device)
+        for fn in (module.gemv_union, module.gemv_sorted):
+            got = fn(x, sorted_ids, toks)[inv].reshape(pair.shape)
+            assert np.array_equal(_bits(got), _bits(pair))
+
+
+@pytest.mark.parametrize("member", IQ2)
+@pytest.mark.parametrize("n", (2048, 4096))
+@pytest.mark.parametrize("out", (OUT, 48))
+def test_sorted_gemv_is_bit_identical_to_the_pair_gemv(device, member, n, out):
+    module, _ = _module(member, n, wirepack.seed_for(member, n, "adj"), device, out=out)
+    rng = np.random.default_rng(91)
+    tokens, top_k = 6, 6
+    idx = rng.integers(0, 5, size=(tokens, top_k)).astype(np.int32)
+    x = torch.from_numpy(rng.standard_normal((tokens, 1, 1, n)).astype(np.float16)).to(device)
+    pair = module.gemv(x, torch.from_numpy(idx).to(device))
+    sorted_ids, toks, _order, inv = _union_operands(idx, top_k, device)
+    got = module.gemv_sorted(x, sorted_ids, toks)
+    assert np.array_equal(_bits(got[inv].reshape(pair.shape)), _bits(pair))
+
+
+@pytest.mark.parametrize("method", ("gemv_sorted", "gemv_union"))
+@pytest.mark.parametrize("member", IQ2)
+def test_sorted_and_union_refuse_a_toks_pair_mismatch(device, member, method):
+    module, _ = _module(member, 2048, 93, device)
+    x = torch.zeros((2, 1, 1, 2048), dtype=torch.float16, device=device)
+    sorted_ids = torch.zeros(8, dtype=torch.int32, device=device)
+    toks = torch.zeros(6, dtype=torch.int32, device=device)
+    with pytest.raises(IqkRuntimeError):
+        getattr(module, method)(x, sorted_ids, toks)
+
+
+@pytest.mark.parametrize("method", ("gemv_sorted", "gemv_union"))
+def test_sorted_and_union_refuse_iq1_s_r4(device, method):
+    """The recorded sorted/union formulations cover the IQ2 members only."""
+    module, _ = _module("iq1_s_r4", 2048, 95, device)
+    x = torch.zeros((2, 1, 1, 2048), dtype=torch.float16, device=device)
+    ids = torch.zeros(4, dtype=torch.int32, device=device)
+    with pytest.raises(IqkKernelError):
+        getattr(module, method)(x, ids, ids)
+
+
+@pytest.mark.parametrize("method", ("gemv_sorted", "gemv_union"))
+@pytest.mark.parametrize("out", (OUT, 48))
+def test_sorted_and_union_mark_out_of_range_rows(device, method, out):
+    """A token row beyond x, or an id beyond the stack, gives a NaN output
+    row and reads nothing out of bounds; the other rows are unaffected."""
+    module, _ = _module("iq2_ks", 2048, 97, device, out=out)
+    rng = np.random.default_rng(99)
+    x = torch.from_numpy(rng.standard_normal((3, 1, 1, 2048)).astype(np.float16)).to(device)
+    ids = torch.tensor([1, 1, 1, 2, EXPERTS, 5], dtype=torch.int32, device=device)
+    toks = torch.tensor([0, 3, 2, 1, 0, 2], dtype=torch.int32, device=device)
+    got = getattr(module, method)(x, ids, toks)
+    bad = torch.tensor([False, True, False, False, True, False])
+    assert torch.isnan(got[bad.to(device)]).all()
+    good_ids = torch.tensor([[1], [1], [2], [5]], dtype=torch.int32, device=device)
+    good_x = x.reshape(3, -1)[torch.tensor([0, 2, 1, 2], device=device)].reshape(4, 1, 1, -1)
+    want = module.gemv(good_x, good_ids).reshape(4, out)
+    assert np.array_equal(_bits(got[(~bad).to(device)]), _bits(want))
+
+
+def test_union_gemv_at_the_routed_geometry(device):
+    """256 experts, gate/up geometry, the multi-token verify shape (4 tokens x
+    top-6 over few experts): bit-identical to the pair GEMV."""
+    print("union gemv routed geometry", flush=True)
+    member, E, out, n = "iq2_ks", 256, 2048, 4096
+    wire = wirepack.random_wire(member, E * out, n, seed=2025, scales="serving")
+    shapes = fmt.component_shapes(member, E, out, n)
+    module = IqkSwitchLinear(member, E, out, n, device=device)
+    module.load_streams({k: np.ascontiguousarray(v).reshape(shapes[k])
+                         for k, v in fmt.pack(member, wire, n).items()})
+    rng = np.random.default_rng(8)
+    tokens, top_k = 4, 6
+    pool = rng.choice(E, 9, replace=False)
+    idx = np.stack([rng.choice(pool, top_k, replace=False) for _ in range(tokens)]).astype(np.int32)
+    x = torch.from_numpy(rng.standard_normal((tokens, 1, 1, n)).astype(np.float16)).to(device)
+    pair = module.gemv(x, torch.from_numpy(idx).to(device))
+    sorted_ids, toks, _order, inv = _union_operands(idx, top_k, device)
+    for fn in (module.gemv_union, module.gemv_sorted):
+        got = fn(x, sorted_ids, toks)[inv].reshape(pair.shape)
+        assert np.array_equal(_bits(got), _bits(pair))
+
+
+# -- range producer and range matmul (reference: tests/test_nn.py:329-377) --
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+@pytest.mark.parametrize("n", (2048, 4096))
+def test_dequantized_range_matches_the_full_slice(device, member, n):
+    module, _ = _module(member, n, wirepack.seed_for(member, n, "range"), device)
+    full = _bits(module.dequantized())
+    for start, rows in ((0, 8), (8, 8), (16, 16), (0, 32), (24, 8), (3, 1), (5, 2), (0, OUT), (128, 128)):
+        got = _bits(module.dequantized_range(start, rows))
+        assert got.shape == (EXPERTS, rows, n), (start, rows)
+        assert np.array_equal(got, full[:, start:start + rows]), (start, rows)
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+def test_dequantized_range_refuses_a_bad_range(device, member):
+    module, _ = _module(member, 2048, 61, device, out=32)
+    for start, rows in ((0, 0), (0, 12), (0, -8), (-8, 8), (28, 8), (0, 64)):
+        with pytest.raises(IqkRuntimeError):
+            module.dequantized_range(start, rows)
+        with pytest.raises(IqkRuntimeError):
+            module.sorted_matmul_range(torch.zeros((1, 1, 2048), dtype=torch.float16, device=device),
+                                       torch.zeros(1, dtype=torch.int32, device=device), start, rows)
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+@pytest.mark.parametrize("n", (2048, 4096))
+def test_sorted_matmul_range_concat_matches_the_sorted_call(device, member, n):
+    """Range outputs concatenated along features equal the unsplit call, bit
+    for bit; ranges narrower than one 16-column MFMA fragment included."""
+    module, _ = _module(member, n, wirepack.seed_for(member, n, "nsplit"), device)
+    rng = np.random.default_rng(67)
+    tokens, top_k = 24, 4
+    x = torch.from_numpy(rng.standard_normal((tokens, 1, 1, n)).astype(np.float16)).to(device)
+    idx = np.sort(rng.integers(0, EXPERTS, size=(tokens, top_k)), axis=None).reshape(tokens, top_k)
+    idx = torch.from_numpy(idx.astype(np.int32)).to(device)
+    full = module(x, idx, sorted_indices=True)
+    half = OUT // 2
+    parts = torch.cat([module.sorted_matmul_range(x, idx, 0, half),
+                       module.sorted_matmul_range(x, idx, half, half)], dim=-1)
+    assert np.array_equal(_bits(parts), _bits(full))
+    narrow = torch.cat([module.sorted_matmul_range(x, idx, 64 + 8 * i, 8) for i in range(2)]
+                       + [module.sorted_matmul_range(x, idx, 80, 1)], dim=-1)
+    assert np.array_equal(_bits(narrow), _bits(full[..., 64:81]))
