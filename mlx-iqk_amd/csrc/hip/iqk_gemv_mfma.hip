@@ -136,7 +136,14 @@ __device__ __forceinline__ uint32_t half_row_mirror(uint32_t v) {
     return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x141, 0xF, 0xF, false));
 }
 
-__device__ __forceinline__ int digits_sum(int4_t d) { return d.x + (d.y << 8) + (d.z << 16); }
+__device__ __forceinline__ int digits_sum(int4_t d) { return (((d.z << 8) + d.y) << 8) + d.x; }
+
+// Keeps a value computed where it stands.  The masked A reads split a decode
+// into one block per super-block, and without a use in its own block each
+// fold would be sunk behind the last stream word, into every wavefront's tail.
+__device__ __forceinline__ void pin(float &v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(uint32_t &v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(int &v) { asm volatile("" : "+v"(v)); }
 
 // IQ1_S_R4's grid expanded to int8 weights 8 * (g + 1/8) = 8g + 1, eight per
 // entry in weight order (two little-endian words), built at compile time from
@@ -314,9 +321,22 @@ struct LaneIq2ks {
         const uint32_t hbg = hb >> (2 * g), abg = ab >> (2 * g);
         const uint32_t scg[4] = {sc.x >> (8 * g), sc.y >> (8 * g), sc.z >> (8 * g), sc.w >> (8 * g)};
         float acc = 0.f;
-        float2 upv[4];  // 2^-E of sub-blocks 8s+2g, 8s+2g+1, read before the loop
+        // Scale index x 2^-E and alphabet pool of sub-blocks 8s+2g+h, formed
+        // from the scale bytes alone (left to the scheduler: pinning them
+        // here measured slower), so the code words meet only their expansion,
+        // the MFMAs and the folds.
+        float fac[4][2];
+        uint32_t pool[4][2];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) upv[s] = *reinterpret_cast<const float2 *>(sbs + 8 * s + 2 * g);
+        for (int s = 0; s < 4; ++s) {
+            const float2 up = *reinterpret_cast<const float2 *>(sbs + 8 * s + 2 * g);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int idx = int(((scg[s] >> (4 * h)) & 15u) | (((hbg >> (8 * s + h)) & 1u) << 4)) - 16;
+                fac[s][h] = float(idx) * (h ? up.y : up.x);
+                pool[s][h] = pick_pool(abg, 8 * s + h, kV8Base, kV8Shift);
+            }
+        }
         int4_t Dp[2], A[4] = {};
 #pragma unroll
         for (int s = 0; s <= 4; ++s) {
@@ -325,19 +345,15 @@ struct LaneIq2ks {
                 read_a(A, abase + 256 * s, data);
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    const uint32_t pool = pick_pool(abg, 8 * s + h, kV8Base, kV8Shift);
-                    D[h] = mfma(A[2 * h], codes_to_i8(q[s][2 * h], pool), int4_t{0, 0, 0, 0});
-                    D[h] = mfma(A[2 * h + 1], codes_to_i8(q[s][2 * h + 1], pool), D[h]);
+                    D[h] = mfma(A[2 * h], codes_to_i8(q[s][2 * h], pool[s][h]), int4_t{0, 0, 0, 0});
+                    D[h] = mfma(A[2 * h + 1], codes_to_i8(q[s][2 * h + 1], pool[s][h]), D[h]);
                 }
             }
             if (s > 0) {  // fold the previous super-block while this one's MFMAs run
                 const int sp = s - 1;
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const float up = h ? upv[sp].y : upv[sp].x;
-                    const int idx = int(((scg[sp] >> (4 * h)) & 15u) | (((hbg >> (8 * sp + h)) & 1u) << 4)) - 16;
-                    acc = fmaf(float(digits_sum(Dp[h])), float(idx) * up, acc);
-                }
+                for (int h = 0; h < 2; ++h) acc = fmaf(float(digits_sum(Dp[h])), fac[sp][h], acc);
+                pin(acc);
             }
             if (s < 4) { Dp[0] = D[0]; Dp[1] = D[1]; }
         }
@@ -386,36 +402,40 @@ struct LaneIq2k {
         // alphabet bits of super-block s: byte 2s + g/2 of ex, bits 4(g%2) + j
         const int exs = 8 * (g >> 1) + 4 * (g & 1);
         const uint32_t exg[2] = {ex.x >> exs, ex.y >> exs};
-        float acc = 0.f, offp = 0.f;
-        float upk[4];  // 2^-E and word sums of this lane's spans, read before the loop
-        float4 fwv[4];
+        // Before any code word is needed: each super-block's d x 2^-E, its
+        // constant part sum_j (idx off)_j fw_j, and its four word pools.
+        float acc = 0.f, dfac[4], offs[4];
+        uint32_t pools[4][4];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            upk[s] = sbs[4 * s + g];
-            fwv[s] = *reinterpret_cast<const float4 *>(fw + 16 * s + 4 * g);
+            const float4 fwv = *reinterpret_cast<const float4 *>(fw + 16 * s + 4 * g);
+            dfac[s] = half_bits_to_float((dv[s >> 1] >> (16 * (s & 1))) & 0xffffu) * sbs[4 * s + g];
+            offs[s] = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t nib = (scw[s] >> (4 * j)) & 15u;
+                const uint32_t alpha = (exg[s >> 1] >> (16 * (s & 1) + j)) & 1u;
+                const uint2_t e = ktab[alpha * 16 + nib];
+                pools[s][j] = e.x;
+                offs[s] = fmaf(__uint_as_float(e.y), fwv[j], offs[s]);
+            }
         }
         int4_t Wp;
 #pragma unroll
         for (int s = 0; s <= 4; ++s) {
             int4_t W = {0, 0, 0, 0};
-            float off = 0.f;
             if (s < 4) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t nib = (scw[s] >> (4 * j)) & 15u;
-                    const uint32_t alpha = (exg[s >> 1] >> (16 * (s & 1) + j)) & 1u;
-                    const uint2_t e = ktab[alpha * 16 + nib];
-                    W = mfma(read_a_all(abase + 256 * s + 16 * j), codes_to_i8(q[s][j], e.x), W);
-                    off = fmaf(__uint_as_float(e.y), fwv[s][j], off);
-                }
+                for (int j = 0; j < 4; ++j)
+                    W = mfma(read_a_all(abase + 256 * s + 16 * j), codes_to_i8(q[s][j], pools[s][j]), W);
             }
             if (s > 0) {  // fold the previous super-block while this one's MFMAs run
                 const int sp = s - 1;
                 const float sum = fmaf(float(Wp.z), 65536.f, fmaf(float(Wp.y), 256.f, float(Wp.x)));
-                const float d = half_bits_to_float((dv[sp >> 1] >> (16 * (sp & 1))) & 0xffffu);
-                acc = fmaf(fmaf(2.f, sum, offp), d * upk[sp], acc);
+                acc = fmaf(fmaf(2.f, sum, offs[sp]), dfac[sp], acc);
+                pin(acc);
             }
-            if (s < 4) { Wp = W; offp = off; }
+            if (s < 4) Wp = W;
         }
         return acc;
     }
@@ -473,25 +493,32 @@ struct LaneIq1s {
     // 8g - 1, which takes 2 sum(f) off its digit sum.
     __device__ __forceinline__ float decode(const uint8_t *abase, bool data, const float *sbs, const int *fsum,
                                             const uint2_t *b8, int g) const {
-        float acc = 0.f;
-        float4 upv[NI];  // 2^-E and sum(f) of blocks 16i+4g+b, read before the loop
-        int4_t fsv[NI];
+        // Before any index byte is needed: each block's scale x 2^-E and its
+        // negative-shift correction 2 sum(f) (or 0).
+        float acc = 0.f, fac[4 * NI];
+        int corr[4 * NI];
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            upv[i] = *reinterpret_cast<const float4 *>(sbs + 16 * i + 4 * g);
-            fsv[i] = *reinterpret_cast<const int4_t *>(fsum + 16 * i + 4 * g);
+            const float4 upv = *reinterpret_cast<const float4 *>(sbs + 16 * i + 4 * g);
+            const int4_t fsv = *reinterpret_cast<const int4_t *>(fsum + 16 * i + 4 * g);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const uint32_t hw = (qh[i][b >> 1] >> (16 * (b & 1))) & 0xffffu;
+                fac[4 * i + b] = float(2 * ((hw >> 12) & 7u) + 1) * upv[b];
+                corr[4 * i + b] = (2 * fsv[b]) & -int(hw >> 15);
+                pin(fac[4 * i + b]);
+                pin(corr[4 * i + b]);
+            }
         }
         int4_t Dp, A[4] = {};
-        uint32_t hp = 0;
 #pragma unroll
         for (int c = 0; c <= 4 * NI; ++c) {  // block c = 4i + b
             int4_t D;
-            uint32_t hw = 0;
             if (c < 4 * NI) {
                 const int i = c >> 2, b = c & 3;
                 if ((b & 1) == 0) read_a(A, abase + 512 * i + 32 * b, data);  // blocks b, b+1
                 const uint32_t qw = qv[i][b];
-                hw = (qh[i][b >> 1] >> (16 * (b & 1))) & 0xffffu;
+                const uint32_t hw = (qh[i][b >> 1] >> (16 * (b & 1))) & 0xffffu;
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {  // 8-weight groups 2t, 2t+1 of the block
                     const uint32_t i0 = ((qw >> (16 * t)) & 0xffu) | (((hw >> (6 * t)) & 7u) << 8);
@@ -502,13 +529,10 @@ struct LaneIq1s {
                 }
             }
             if (c > 0) {
-                const int cp = c - 1;
-                const int neg = int(hp >> 15);
-                const int sint = digits_sum(Dp) - ((2 * fsv[cp >> 2][cp & 3]) & -neg);
-                const float ls = float(2 * ((hp >> 12) & 7u) + 1);
-                acc = fmaf(float(sint), ls * upv[cp >> 2][cp & 3], acc);
+                acc = fmaf(float(digits_sum(Dp) - corr[c - 1]), fac[c - 1], acc);
+                pin(acc);
             }
-            if (c < 4 * NI) { Dp = D; hp = hw; }
+            if (c < 4 * NI) Dp = D;
         }
         return acc * (0.125f * half_bits_to_float(dvb));
     }
