@@ -301,7 +301,7 @@ def prefill_cell(torch, device, args, seed: int):
     res = {"tokens": tokens, "pairs": int(flat.size), "experts_routed": int((counts > 0).sum()),
            "max_pairs_per_expert": int(counts.max()), "projections": {}}
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
-    tot_prod = tot_gemm = 0.0
+    tot_prod = tot_gemm = tot_fused = 0.0
     tot_bytes = tot_flop = 0
     for name, member, (out, n), xin in projections:
         mod = IqkSwitchLinear(member, EXPERTS, out, n, device=device)
@@ -321,14 +321,21 @@ def prefill_cell(torch, device, args, seed: int):
             0, slot[ids.long()].long(), torch.ones_like(ids, dtype=torch.int64)), 0).to(torch.int32)
         rows = torch.arange(flat.size, dtype=torch.int32, device=device)
         w = torch.empty((n_slots, out, n), dtype=torch.float16, device=device)
+        # the fused route's operands: experts as groups, pairs already sorted
+        offs_e = torch.zeros(EXPERTS + 1, dtype=torch.int32, device=device)
+        offs_e[1:] = torch.from_numpy(np.cumsum(counts).astype(np.int32)).to(device)
+        yf = torch.empty((flat.size, out), dtype=torch.float16, device=device)
         reps = 3
-        times = {"producer": [], "floor": [], "gemm": []}
+        times = {"producer": [], "floor": [], "gemm": [], "fused": []}
         for _ in range(reps):
-            for key in ("producer", "floor", "gemm"):
+            for key in ("producer", "floor", "gemm", "fused"):
                 a, b = ev(), ev()
                 a.record()
                 if key == "gemm":
                     kernels.grouped_gemm(xin.reshape(-1, n), w, offs, rows)
+                elif key == "fused":
+                    kernels.fused_matmul(member, xin.reshape(-1, n), mod._streams(), EXPERTS, out, offs_e, rows,
+                                         out=yf)
                 else:
                     kernels.dequant(member, mod._streams(), EXPERTS, out, n, slot_of_expert=slot, n_slots=n_slots,
                                     out=w, floor=(key == "floor"))
@@ -336,6 +343,9 @@ def prefill_cell(torch, device, args, seed: int):
                 b.synchronize()
                 times[key].append(a.elapsed_time(b) * 1e3)
         med = {k: statistics.median(v) for k, v in times.items()}
+        kernels.dequant(member, mod._streams(), EXPERTS, out, n, slot_of_expert=slot, n_slots=n_slots, out=w)
+        yp = kernels.grouped_gemm(xin.reshape(-1, n), w, offs, rows).float()  # the producer route's output
+        fused_dev = ((yf.float() - yp).abs().max() / yp.abs().max()).item()
         nbytes = routed * out * (fmt.ik_row_bytes(member, n) + 2 * n)
         flop = 2 * flat.size * out * n
         r = {"member": member, "experts_reconstructed": routed,
@@ -346,18 +356,26 @@ def prefill_cell(torch, device, args, seed: int):
              "gemm_us": round(med["gemm"], 2), "gemm_flop": flop,
              "gemm_tflops": round(flop / (med["gemm"] * 1e-6) / 1e12, 2)}
         r["mfma_utilisation"] = round(r["gemm_tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
+        r.update({"fused_us": round(med["fused"], 2), "fused_tflops": round(flop / (med["fused"] * 1e-6) / 1e12, 2),
+                  "fused_speedup_over_producer_route": round((med["producer"] + med["gemm"]) / med["fused"], 2),
+                  "fused_max_dev_vs_producer_route": round(fused_dev, 6)})
+        r["fused_mfma_utilisation"] = round(r["fused_tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
         res["projections"][name] = r
+        tot_fused += med["fused"]
         tot_prod += med["producer"]
         tot_gemm += med["gemm"]
         tot_bytes += nbytes
         tot_flop += flop
         log(f"  {name}: producer {med['producer']:.1f} us ({r['producer_gb_per_s']} GB/s, x{r['producer_x_floor']})"
-            f"  gemm {med['gemm']:.1f} us ({r['gemm_tflops']} TFLOP/s)")
-        del mod, w, y
+            f"  gemm {med['gemm']:.1f} us ({r['gemm_tflops']} TFLOP/s)"
+            f"  fused {med['fused']:.1f} us ({r['fused_tflops']} TFLOP/s, dev {fused_dev:.2e})")
+        del mod, w, y, yf, yp
         torch.cuda.empty_cache()
     res["producer_gb_per_s"] = round(tot_bytes / (tot_prod * 1e-6) / 1e9, 1)
     res["gemm_tflops"] = round(tot_flop / (tot_gemm * 1e-6) / 1e12, 2)
     res["mfma_utilisation"] = round(res["gemm_tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
+    res["fused_tflops"] = round(tot_flop / (tot_fused * 1e-6) / 1e12, 2)
+    res["fused_mfma_utilisation"] = round(res["fused_tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
     return res
 
 

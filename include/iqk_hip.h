@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define IQK_HIP_ABI_VERSION 2
+#define IQK_HIP_ABI_VERSION 3
 
 #define IQK_MEMBER_IQ2_KS 0
 #define IQK_MEMBER_IQ2_K 1
@@ -146,6 +146,26 @@ int iqk_dequant_floor(int member, int64_t in_features, int64_t out_features, int
 int iqk_grouped_gemm(int64_t in_features, int64_t out_features, int64_t n_groups, int64_t n_slots,
                      const void *x, int64_t n_x_rows, const void *w, const uint32_t *group_offsets,
                      const uint32_t *x_rows, const uint32_t *y_rows, void *y, void *stream);
+
+// Fused prefill contraction straight from the streams: the producer's fp16
+// weights formed inside an fp16 MFMA grouped GEMM, never stored (replaces
+// dequant_kernel / dequant_range_kernel + mx.gather_mm(x, W.swapaxes(-1,-2),
+// rhs_indices, sorted_indices=True), src/mlx_iqk/nn.py:155-238).  Slots are
+// sorted by expert; expert e owns slots [group_offsets[e], group_offsets[e+1]):
+//   y[y_rows[p]][n] = fp16( sum_k x[x_rows[p]][k] * W[e][row_start + n][k] ),
+// 0 <= n < rows, with W iqk_dequant's fp16 value bit for bit and f32
+// accumulation (the summation order differs from iqk_dequant +
+// iqk_grouped_gemm; it does not depend on row_start, so row ranges
+// concatenate to the full call bit for bit).  y: f16 [n_slots, rows];
+// group_offsets: u32 [num_experts + 1] (device, non-decreasing, last =
+// n_slots); x, x_rows, y_rows as iqk_grouped_gemm.  IQK_ERR_GEOMETRY unless
+// 0 <= row_start < row_start + rows <= out_features.  IQK_MEMBER_IQ2_KS and
+// IQK_MEMBER_IQ2_K; IQ1_S_R4 returns IQK_ERR_MEMBER.
+int iqk_fused_gemm(int member, int64_t in_features, int64_t out_features, int64_t num_experts,
+                   const void *x, int64_t n_x_rows, const void *const *streams, int n_streams,
+                   int64_t row_start, int64_t rows, const uint32_t *group_offsets,
+                   const uint32_t *x_rows, const uint32_t *y_rows, int64_t n_slots,
+                   void *y, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,322 @@
+// Fused dequant-in-MFMA grouped GEMM: the prefill contraction straight from
+// the relayout streams (gfx950, fp16 MFMA, f32 accumulation).
+//
+// Reference: the prefill route dequantizes the whole stack to fp16
+// (src/mlx_iqk/nn.py:155-169) and contracts it with mx.gather_mm over the
+// sorted pairs (nn.py:221-238).  Here each workgroup decodes the weight rows
+// it needs straight into MFMA operands, so a prefill reads the 2-bit streams
+// (1122 B per 4096-wide IQ2_KS row) instead of writing and re-reading 8 KiB of
+// fp16 per row.  The weights are the producer's fp16 values bit for bit (the
+// same four-entry tables); only the f32 summation order differs from the
+// producer + grouped GEMM route.
+//
+// Work list: as the grouped GEMM, with group g = expert g: the slots (pair
+// rows) are sorted by expert, expert g owns [offs[g], offs[g+1]), and a block
+// takes one M-tile t of the list (64 slots) and one column block c (weight
+// rows [256c, 256c + 256) of the requested row range).  Blocks are dealt to
+// the eight XCDs in turn, so block b runs on XCD b % 8; the mapping gives
+// XCD b % 8 the column blocks of M-tile 8 (b / (8 C)) + b % 8 one after
+// another (C column blocks), and the activations they share stay in that
+// XCD's L2.
+//
+// Tile: 256 threads, four wavefronts.  Wavefront w owns weight rows
+// 64w .. 64w+63 of the block (four 16-column MFMA blocks j) for all 64 slots
+// (four 16-row MFMA blocks i): 16 accumulators of v_mfma_f32_16x16x32_f16.
+// Reduction steps of 128: lane (n, kg) = (l % 16, l / 16) decodes the 32
+// weights of sub-block kg of the step (k = 128s + 32kg .. +32) of its row and
+// feeds them to the step's four MFMAs t as weights 8t .. 8t+7 (in the order
+// (0,4,1,5,2,6,3,7) that the byte-split table lookup produces; the staged
+// activations are permuted to match).  A lane thus builds its fp16 table once
+// per 32 weights, and the MFMA's k index maps to the same weight for A and B.  The step's activations (64 slots x 128 fp16)
+// are staged in LDS, double buffered, one barrier per step; the code words of
+// the next step are loaded while this one computes.  The block's scale planes
+// (all 256 rows, whole reduction axis) are copied to LDS once, rows padded so
+// the 16 rows a wavefront reads at once fall in distinct banks.
+
+#include "iqk_device.h"
+#include "iqk_host.h"
+#include "iqk_pool.h"
+
+namespace iqk {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+
+constexpr int kFusedBM = 64;    // slots per block
+constexpr int kFusedBN = 256;   // weight rows per block
+constexpr int kFusedKS = 128;   // reduction elements per step
+constexpr int kXStride = 2 * kFusedKS + 16;  // LDS bytes per staged activation row
+
+struct FusedArgs {
+    const uint16_t *x;
+    const void *s0, *s1, *s2, *s3, *s4;
+    const uint32_t *offs;  // [n_groups + 1]
+    const uint32_t *xr, *yr;
+    uint16_t *y;
+    uint32_t N;         // output columns: weight rows row_start .. row_start + N of each expert
+    uint32_t out_rows;  // rows per expert in the streams
+    uint32_t row_start;
+    uint32_t n_groups, n_slots, n_x_rows;
+};
+
+// A block's scale planes in LDS.  IQ2_KS: scl u8 [K/64], sch u8 [K/256],
+// sex u8 [K/256], dv f16 per row.  IQ2_K: scl u16 [K/64], sex u8 [K/128],
+// dv f16 [K/256].  Row strides are padded to an odd number of dwords.
+template <int MEMBER, int K>
+struct FusedScales {
+    static constexpr bool KS = MEMBER == IQ2_KS;
+    static constexpr int SCL = KS ? K / 64 : K / 32;    // bytes per row
+    static constexpr int HB = KS ? K / 256 : 0;
+    static constexpr int EX = KS ? K / 256 : K / 128;
+    static constexpr int DV = KS ? 2 : K / 128;
+    static constexpr int pad(int b) { return b == 0 ? 0 : ((b + 3) / 4 % 2 ? (b + 3) / 4 * 4 : (b + 3) / 4 * 4 + 4); }
+    static constexpr int SCL_S = pad(SCL), HB_S = pad(HB), EX_S = pad(EX), DV_S = pad(DV);
+    uint8_t scl[kFusedBN * SCL_S];
+    uint8_t hb[KS ? kFusedBN * HB_S : 4];
+    uint8_t ex[kFusedBN * EX_S];
+    uint8_t dv[kFusedBN * DV_S];
+};
+
+// Copy `rows` rows of a plane (bytes_per_row each, consecutive in global
+// memory) into LDS rows of `stride` bytes, in 16-bit units (every plane's row
+// is a whole number of them).
+__device__ __forceinline__ void copy_plane(const uint8_t *src, int rows, int bytes_per_row, uint8_t *dst, int stride,
+                                           int tid) {
+    const int units_per_row = bytes_per_row / 2;
+    const int units = rows * units_per_row;
+    for (int u = tid; u < units; u += 256) {
+        const int r = u / units_per_row, c = u - r * units_per_row;
+        *reinterpret_cast<uint16_t *>(dst + r * stride + 2 * c) = reinterpret_cast<const uint16_t *>(src)[u];
+    }
+}
+
+// The two v_perm tables of lane (row, kg) at step s: one per 16-weight word
+// of its 32 weights (IQ2_KS: both from sub-block 4s + kg; IQ2_K: sub-blocks
+// 8s + 2kg and 8s + 2kg + 1).  Same f32 chain as the producer.
+template <int MEMBER, int K>
+__device__ __forceinline__ void fused_pools(const FusedScales<MEMBER, K> &sc, int row, int s, int kg, Pool &p0,
+                                            Pool &p1) {
+    using S = FusedScales<MEMBER, K>;
+    if constexpr (MEMBER == IQ2_KS) {
+        const int sb = 4 * s + kg;
+        const uint32_t scl = sc.scl[row * S::SCL_S + (sb >> 1)];
+        const uint32_t hb = sc.hb[row * S::HB_S + (sb >> 3)];
+        const uint32_t ab = sc.ex[row * S::EX_S + (sb >> 3)];
+        const uint32_t dvb = *reinterpret_cast<const uint16_t *>(sc.dv + row * S::DV_S);
+        const int idx = int(((scl >> (4 * (sb & 1))) & 15u) | (((hb >> (sb & 7)) & 1u) << 4)) - 16;
+        const bool alpha = (ab >> (sb & 7)) & 1u;
+        const float dl = half_bits_to_float(dvb) * float(idx);
+        p0 = make_pool(dl, alpha ? -26.f : -31.f, alpha ? -8.f : -13.f, alpha ? 6.f : 1.f, alpha ? 22.f : 17.f);
+        p1 = p0;
+    } else {
+        const int sb = 8 * s + 2 * kg;  // first of the lane's two 16-weight sub-blocks
+        const uint32_t scw = *reinterpret_cast<const uint16_t *>(sc.scl + row * S::SCL_S + 2 * (sb >> 2));
+        const uint32_t ab = sc.ex[row * S::EX_S + (sb >> 3)];
+        const uint32_t dvb = *reinterpret_cast<const uint16_t *>(sc.dv + row * S::DV_S + 2 * (sb >> 4));
+        const float d = half_bits_to_float(dvb);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int idx = int((scw >> (4 * ((sb + h) & 3))) & 15u) - 8;
+            const bool alpha = (ab >> ((sb + h) & 7)) & 1u;
+            const float dl = d * float(idx);
+            (h ? p1 : p0) =
+                make_pool(dl, alpha ? -26.f : -31.f, alpha ? -8.f : -13.f, alpha ? 6.f : 1.f, alpha ? 22.f : 17.f);
+        }
+    }
+}
+
+template <int MEMBER, int K>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void fused_gemm_kernel(FusedArgs a) {
+    using S = FusedScales<MEMBER, K>;
+    constexpr int STEPS = K / kFusedKS;
+    __shared__ TileScan ts;
+    __shared__ __attribute__((aligned(16))) uint8_t xs[2][kFusedBM * kXStride];
+    __shared__ __attribute__((aligned(16))) S sc;
+
+    const int tid = threadIdx.x;
+    const uint32_t ncb = (a.N + kFusedBN - 1) / kFusedBN;  // column blocks
+    const uint32_t bq = blockIdx.x >> 3, xcd = blockIdx.x & 7u;
+    const uint32_t tile = 8 * (bq / ncb) + xcd, cblock = bq % ncb;
+    uint32_t g, mtile;
+    if (!find_mtile<kFusedBM>(a.offs, a.n_groups, tile, ts, g, mtile)) return;  // surplus block
+
+    // Offsets and row indices are device data: a slot outside [0, n_slots)
+    // is never stored, a row outside x is never read (its output row is 0),
+    // and a weight row past out_features is never stored.  Loads of such
+    // rows read an in-bounds row instead, so the step has no branches and the
+    // scheduler can overlap one column block's decode with the MFMAs of the
+    // previous one.
+    const uint32_t gend = min(a.offs[g + 1], a.n_slots);
+    const uint32_t m0 = a.offs[g] + mtile * kFusedBM;
+    const uint32_t n0 = cblock * kFusedBN;
+    const int rows_here = int(min(uint32_t(kFusedBN), a.N - n0));
+    const size_t row0 = size_t(g) * a.out_rows + a.row_start + n0;  // first stacked weight row of the block
+
+    // scale planes of the block's rows
+    copy_plane(static_cast<const uint8_t *>(a.s1) + row0 * S::SCL, rows_here, S::SCL, sc.scl, S::SCL_S, tid);
+    if constexpr (MEMBER == IQ2_KS) {
+        copy_plane(static_cast<const uint8_t *>(a.s2) + row0 * S::HB, rows_here, S::HB, sc.hb, S::HB_S, tid);
+        copy_plane(static_cast<const uint8_t *>(a.s3) + row0 * S::EX, rows_here, S::EX, sc.ex, S::EX_S, tid);
+        copy_plane(static_cast<const uint8_t *>(a.s4) + row0 * S::DV, rows_here, S::DV, sc.dv, S::DV_S, tid);
+    } else {
+        copy_plane(static_cast<const uint8_t *>(a.s2) + row0 * S::EX, rows_here, S::EX, sc.ex, S::EX_S, tid);
+        copy_plane(static_cast<const uint8_t *>(a.s3) + row0 * S::DV, rows_here, S::DV, sc.dv, S::DV_S, tid);
+    }
+
+    // activation staging: thread t moves 64 bytes of slot row t/4 per step
+    const int xrow_l = tid >> 2, xseg = tid & 3;
+    const uint32_t xp = m0 + uint32_t(xrow_l);
+    const uint32_t xrow = xp < gend ? a.xr[xp] : a.n_x_rows;
+    const bool xv = xrow < a.n_x_rows;
+    const uint8_t *xsrc = reinterpret_cast<const uint8_t *>(a.x) + (size_t(xv ? xrow : 0u) * K + 32 * xseg) * 2;
+    const auto load_x = [&](int s, uint4_t *v) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = load_u4(xsrc + 2 * kFusedKS * s + 16 * i);
+    };
+    // Each 8-element chunk is stored in the order (0,4,1,5,2,6,3,7), the
+    // order expand_word_paired gives the weights.
+    const auto store_x = [&](int buf, const uint4_t *v) {
+        uint8_t *dst = xs[buf] + xrow_l * kXStride + 64 * xseg;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<uint4_t *>(dst + 16 * i) =
+                uint4_t{perm(v[i].z, v[i].x, 0x05040100u), perm(v[i].z, v[i].x, 0x07060302u),
+                        perm(v[i].w, v[i].y, 0x05040100u), perm(v[i].w, v[i].y, 0x07060302u)};
+    };
+
+    // this lane's weight rows (one per column block j) and code words
+    const int wave = tid >> 6, l = tid & 63, ln = l & 15, kg = l >> 4;
+    int lrow[4];
+    bool wv[4];
+    const uint8_t *qsrc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        lrow[j] = 64 * wave + 16 * j + ln;
+        wv[j] = lrow[j] < rows_here;
+        qsrc[j] = static_cast<const uint8_t *>(a.s0) + ((row0 + (wv[j] ? lrow[j] : 0)) * (K / 4) + 8 * kg);
+    }
+    const auto load_q = [&](int s, uint2_t *q) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[j] = *reinterpret_cast<const uint2_t *>(qsrc[j] + 32 * s);
+    };
+
+    uint4_t xa[4];
+    uint2_t q[4], qn[4];
+    load_x(0, xa);
+    load_q(0, q);
+    store_x(0, xa);
+    __syncthreads();  // scale planes and the first activations are in LDS
+
+    float4_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    for (int s = 0; s < STEPS; ++s) {
+        const bool more = s + 1 < STEPS;
+        if (more) {
+            load_x(s + 1, xa);
+            load_q(s + 1, qn);
+        }
+        const uint8_t *xb = xs[s & 1];
+        half8_t af[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                af[i][t] = __builtin_bit_cast(
+                    half8_t, *reinterpret_cast<const uint4_t *>(xb + (16 * i + ln) * kXStride + 64 * kg + 16 * t));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t bw[16];
+            Pool p0, p1;
+            fused_pools<MEMBER, K>(sc, lrow[j], s, kg, p0, p1);  // rows past out_features: LDS junk, never stored
+            expand_word_paired(q[j].x, p0, bw);
+            expand_word_paired(q[j].y, p1, bw + 8);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                // weights 8t .. 8t+7 in the order (0,4,1,5,2,6,3,7)
+                const uint32_t *w8 = bw + 8 * (t >> 1) + (t & 1);
+                const half8_t bf = __builtin_bit_cast(half8_t, uint4_t{w8[0], w8[2], w8[4], w8[6]});
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i][t], bf, acc[i][j], 0, 0, 0);
+            }
+        }
+        if (more) {
+            store_x((s + 1) & 1, xa);  // the buffer every wavefront finished reading before the last barrier
+#pragma unroll
+            for (int j = 0; j < 4; ++j) q[j] = qn[j];
+        }
+        __syncthreads();
+    }
+
+    // D layout: lane l holds rows 4(l/16) + r of column l % 16.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t p = m0 + 16 * i + 4 * kg + r;
+            const bool pv = p < gend;
+            const uint32_t yrow = pv ? (a.yr ? a.yr[p] : p) : a.n_slots;
+            const bool live = pv && a.xr[pv ? p : 0] < a.n_x_rows;  // its activations were real
+            if (yrow < a.n_slots) {
+                uint16_t *yp = a.y + size_t(yrow) * a.N + n0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (wv[j]) yp[lrow[j]] = live ? uint16_t(float_to_half_bits(acc[i][j][r])) : uint16_t(0);
+            }
+        }
+    }
+}
+
+template <int MEMBER>
+int launch_fused(int64_t k, const FusedArgs &a, uint32_t n_slots, hipStream_t st) {
+    const uint64_t mtiles = (uint64_t(n_slots) + kFusedBM - 1) / kFusedBM + uint64_t(a.n_groups);
+    const uint64_t blocks = (mtiles + 7) / 8 * 8 * ((a.N + kFusedBN - 1) / kFusedBN);
+    if (blocks > 0x7fffffffull) return IQK_ERR_ARGUMENT;
+    const dim3 grid{uint32_t(blocks)}, block{256};
+    if (k == 4096)
+        hipLaunchKernelGGL((fused_gemm_kernel<MEMBER, 4096>), grid, block, 0, st, a);
+    else
+        hipLaunchKernelGGL((fused_gemm_kernel<MEMBER, 2048>), grid, block, 0, st, a);
+    return record_launch(hipGetLastError());
+}
+
+}  // namespace iqk
+
+extern "C" int iqk_fused_gemm(int member, int64_t in_features, int64_t out_features, int64_t num_experts,
+                              const void *x, int64_t n_x_rows, const void *const *streams, int n_streams,
+                              int64_t row_start, int64_t rows, const uint32_t *group_offsets,
+                              const uint32_t *x_rows, const uint32_t *y_rows, int64_t n_slots, void *y,
+                              void *stream) {
+    using namespace iqk;
+    if (!member_ok(member)) return IQK_ERR_MEMBER;
+    if (member == IQK_MEMBER_IQ1_S_R4) return IQK_ERR_MEMBER;  // no fused form (yet): producer + grouped GEMM
+    if (!width_sized(in_features)) return IQK_ERR_GEOMETRY;
+    if (out_features <= 0 || out_features > (int64_t(1) << 24)) return IQK_ERR_GEOMETRY;
+    if (row_start < 0 || rows <= 0 || row_start + rows > out_features) return IQK_ERR_GEOMETRY;
+    if (num_experts <= 0 || num_experts > (int64_t(1) << 20)) return IQK_ERR_ARGUMENT;
+    if (n_slots < 0 || n_slots > (int64_t(1) << 30) || n_x_rows < 0 || n_x_rows > 0xffffffffll)
+        return IQK_ERR_ARGUMENT;
+    if (n_slots == 0) return IQK_OK;
+    if (!x || !y || !group_offsets || !x_rows || !streams_ok(streams, n_streams, member)) return IQK_ERR_ARGUMENT;
+    FusedArgs a;
+    a.x = static_cast<const uint16_t *>(x);
+    a.s0 = streams[0]; a.s1 = streams[1]; a.s2 = streams[2]; a.s3 = streams[3];
+    a.s4 = n_streams > 4 ? streams[4] : nullptr;
+    a.offs = group_offsets;
+    a.xr = x_rows;
+    a.yr = y_rows;
+    a.y = static_cast<uint16_t *>(y);
+    a.N = uint32_t(rows);
+    a.out_rows = uint32_t(out_features);
+    a.row_start = uint32_t(row_start);
+    a.n_groups = uint32_t(num_experts);
+    a.n_slots = uint32_t(n_slots);
+    a.n_x_rows = uint32_t(n_x_rows);
+    hipStream_t st = as_stream(stream);
+    return member == IQK_MEMBER_IQ2_KS ? launch_fused<IQ2_KS>(in_features, a, uint32_t(n_slots), st)
+                                       : launch_fused<IQ2_K>(in_features, a, uint32_t(n_slots), st);
+}

@@ -44,46 +44,15 @@ __device__ __forceinline__ half8_t load_frag(const uint16_t *p) {
 }
 
 __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a) {
-    __shared__ uint32_t scan[256];
-    __shared__ uint32_t s_group, s_mtile, s_total;
+    __shared__ TileScan ts;
     const int tid = threadIdx.x;
-    const uint32_t t = blockIdx.x;
-    if (tid == 0) s_group = 0xffffffffu;
-    uint32_t carry = 0;
-    for (uint32_t base = 0; base < a.n_groups; base += 256) {
-        const uint32_t g = base + tid;
-        uint32_t cnt = 0;
-        if (g < a.n_groups) {
-            const uint32_t c = a.offs[g + 1] - a.offs[g];
-            cnt = (c + kGemmBM - 1) / kGemmBM;
-        }
-        __syncthreads();
-        scan[tid] = cnt;
-        __syncthreads();
-        for (int off = 1; off < 256; off <<= 1) {
-            const uint32_t v = tid >= off ? scan[tid - off] : 0u;
-            __syncthreads();
-            scan[tid] += v;
-            __syncthreads();
-        }
-        const uint32_t incl = carry + scan[tid];
-        const uint32_t excl = incl - cnt;
-        if (cnt && t >= excl && t < incl) {
-            s_group = g;
-            s_mtile = t - excl;
-        }
-        if (tid == 255) s_total = incl;
-        __syncthreads();
-        carry = s_total;
-    }
-    __syncthreads();
-    const uint32_t g = s_group;
-    if (g == 0xffffffffu) return;  // surplus block: beyond the last M-tile
+    uint32_t g, mtile;
+    if (!find_mtile<kGemmBM>(a.offs, a.n_groups, blockIdx.x, ts, g, mtile)) return;  // surplus block
 
     // Offsets and row indices are device data: any slot outside [0, n_slots)
     // or row outside x is skipped (zero operand, no store), never read.
     const uint32_t gend = min(a.offs[g + 1], a.n_slots);
-    const uint32_t m0 = a.offs[g] + s_mtile * kGemmBM;
+    const uint32_t m0 = a.offs[g] + mtile * kGemmBM;
     const int wave = tid / 64, lane = tid % 64;
     const int lr = lane % 16, lk = 8 * (lane / 16);
     const uint32_t n0 = blockIdx.y * kGemmBN + wave * 64;

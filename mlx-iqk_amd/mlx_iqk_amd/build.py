@@ -34,6 +34,7 @@ HIP_SOURCES = {
     "iqk_gemv_mfma.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
     "iqk_dequant.hip": (),
     "iqk_gemm.hip": (),
+    "iqk_fused_gemm.hip": (),
 }
 OFFLOAD_ARCH = "gfx950"
 

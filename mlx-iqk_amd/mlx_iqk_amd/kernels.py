@@ -297,9 +297,54 @@ def grouped_gemm(x: torch.Tensor, w: torch.Tensor, group_offsets: torch.Tensor, 
     return out
 
 
+FUSED_MEMBERS = IQ2_MEMBERS
+"""Members the fused prefill contraction covers."""
+
+
+def fused_matmul(member: str, x: torch.Tensor, streams: list[torch.Tensor], num_experts: int, out_features: int,
+                 group_offsets: torch.Tensor, x_rows: torch.Tensor, y_rows: torch.Tensor | None = None, *,
+                 row_start: int = 0, rows: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Prefill contraction straight from the streams: ``y[y_rows[p]] = x[x_rows[p]] @ W[e, r0:r0+rows]^T``
+    for the slots ``p`` of expert ``e`` (``[group_offsets[e], group_offsets[e+1])``), with
+    ``W`` the producer's fp16 weights formed inside the GEMM.  fp16 ``[P, rows]``."""
+    if member not in FUSED_MEMBERS:
+        raise IqkKernelError(f"the fused prefill covers {FUSED_MEMBERS}; {member!r} takes the producer route")
+    n = int(x.shape[-1])
+    check_dequant_geometry(n, out_features)
+    row_start = int(row_start)
+    rows = out_features - row_start if rows is None else int(rows)
+    if row_start < 0 or rows <= 0 or row_start + rows > out_features:
+        raise IqkKernelError(f"row range [{row_start}, {row_start + rows}) is outside out_features {out_features}")
+    device = check_streams(member, streams, num_experts, out_features, n)
+    _require_cuda(x, "x", torch.float16, device)
+    _require_cuda(group_offsets, "group_offsets", (torch.int32, torch.uint32), device)
+    _require_cuda(x_rows, "x_rows", (torch.int32, torch.uint32), device)
+    if x.dim() != 2 or tuple(group_offsets.shape) != (num_experts + 1,):
+        raise IqkKernelError(f"x must be [rows, {n}] and group_offsets [{num_experts + 1}]")
+    P = int(x_rows.numel())
+    if y_rows is not None:
+        _require_cuda(y_rows, "y_rows", (torch.int32, torch.uint32), device)
+        if y_rows.numel() != P:
+            raise IqkKernelError("y_rows and x_rows must have the same length")
+    if out is None:
+        out = torch.empty((P, rows), dtype=torch.float16, device=device)
+    else:
+        _require_cuda(out, "out", torch.float16, device)
+        if tuple(out.shape) != (P, rows):
+            raise IqkKernelError(f"out must be {(P, rows)}")
+    ptrs = _native.pointer_array([t.data_ptr() for t in streams])
+    rc = _native.load().iqk_fused_gemm(
+        _native.MEMBER_IDS[member], n, out_features, num_experts, x.data_ptr(), int(x.shape[0]), ptrs, len(streams),
+        row_start, rows, group_offsets.data_ptr(), x_rows.data_ptr(), y_rows.data_ptr() if y_rows is not None else None, P,
+        out.data_ptr(), _stream_ptr(device))
+    _native.check(rc, f"iqk_fused_gemm({member}, {n}x{out_features}, P={P})")
+    return out
+
+
 __all__ = [
     "DEQUANT_THREADS", "IQ2_MEMBERS", "MEMBERS", "ROWS_PER_TG",
     "SUPPORTED_IN_FEATURES", "TABLE_INPUT_NAMES", "WEIGHTS_PER_LANE", "IqkKernelError",
     "check_dequant_geometry", "check_gemv_geometry", "check_streams", "dequant", "dequant_input_names",
-    "check_iq2_member", "gemv", "gemv_input_names", "gemv_sorted", "grouped_gemm", "stream_dtypes",
+    "FUSED_MEMBERS", "check_iq2_member", "fused_matmul", "gemv", "gemv_input_names", "gemv_sorted", "grouped_gemm",
+    "stream_dtypes",
 ]

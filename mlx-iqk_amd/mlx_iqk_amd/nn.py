@@ -74,6 +74,10 @@ class IqkSwitchLinear(torch.nn.Module):
     """Stacked IQ_K experts for one projection, ``(x, indices)`` interface."""
 
     mode = "iqk"
+    fused_prefill = True
+    """Prefill through the fused contraction (IQ2 members: the producer's fp16
+    weights formed inside the GEMM, never stored) rather than producer + grouped
+    GEMM.  Both give the same weights; the f32 summation order differs."""
 
     def __init__(self, member: str, num_experts: int, out_features: int, in_features: int,
                  device=None):
@@ -243,22 +247,29 @@ class IqkSwitchLinear(torch.nn.Module):
         xflat = xb.reshape(-1, self.in_features).contiguous()
         xidx = torch.arange(math.prod(xbatch), device=device).reshape(xbatch).broadcast_to(batch).reshape(-1)
         ids = indices.to(device=device, dtype=torch.int64).broadcast_to(batch).reshape(-1)
+        E = self.num_experts
+        order = torch.argsort(ids, stable=True)
+        r = torch.arange(M, device=device)
+        x_rows = (xidx[order][:, None] * M + r).reshape(-1).to(torch.int32)
+        y_rows = (order[:, None] * M + r).reshape(-1).to(torch.int32)
+        if self.fused_prefill and self.member in kernels.FUSED_MEMBERS:
+            counts = torch.zeros(E, dtype=torch.int64, device=device).index_add_(0, ids, torch.full_like(ids, M))
+            offsets = torch.zeros(E + 1, dtype=torch.int32, device=device)
+            offsets[1:] = torch.cumsum(counts, 0).to(torch.int32)
+            y = kernels.fused_matmul(self.member, xflat, self._streams(), E, self.out_features, offsets, x_rows,
+                                     y_rows, row_start=start, rows=rows)
+            return y.reshape(tuple(batch) + (M, rows))
         # Experts are routed only if some pair names them; compact them into
         # slots in expert order.  n_slots is an upper bound known on the host.
-        E = self.num_experts
         present = torch.zeros(E, dtype=torch.int32, device=device).index_fill_(0, ids, 1)
         slot_of_expert = torch.where(present > 0, torch.cumsum(present, 0, dtype=torch.int32) - 1,
                                      torch.full_like(present, -1))
         n_slots = min(E, P)
-        order = torch.argsort(ids, stable=True)
         slot_of_pair = slot_of_expert[ids].to(torch.int64)
         counts = torch.zeros(n_slots, dtype=torch.int64, device=device).index_add_(
             0, slot_of_pair, torch.full_like(slot_of_pair, M))
         offsets = torch.zeros(n_slots + 1, dtype=torch.int32, device=device)
         offsets[1:] = torch.cumsum(counts, 0).to(torch.int32)
-        r = torch.arange(M, device=device)
-        x_rows = (xidx[order][:, None] * M + r).reshape(-1).to(torch.int32)
-        y_rows = (order[:, None] * M + r).reshape(-1).to(torch.int32)
         w = kernels.dequant(self.member, self._streams(), E, self.out_features, self.in_features,
                             slot_of_expert=slot_of_expert, n_slots=n_slots, row_start=start, rows=rows)
         y = kernels.grouped_gemm(xflat, w, offsets, x_rows, y_rows)

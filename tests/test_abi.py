@@ -112,3 +112,18 @@ def test_sorted_union_and_range_entry_points_refuse_bad_arguments(lib):
         assert lib.iqk_dequant_rows(0, 2048, 32, 4, streams, 5, start, rows, None, 4, p, None) == _native.ERR_GEOMETRY
     assert lib.iqk_dequant_rows(0, 2048, 32, 4, streams, 5, 0, 32, None, 3, p, None) == _native.ERR_ARGUMENT
     assert lib.iqk_dequant_rows(0, 2048, 32, 4, streams, 5, 0, 32, p, 0, p, None) == _native.OK
+
+
+def test_fused_gemm_refuses_bad_arguments(lib):
+    p = ctypes.c_void_p(16)  # never dereferenced: every call below is refused first
+    streams = _native.pointer_array([16] * 5)
+    f = lib.iqk_fused_gemm
+    assert f(2, 4096, 2048, 8, p, 4, streams, 3, 0, 2048, p, p, None, 4, p, None) == _native.ERR_MEMBER
+    assert f(7, 4096, 2048, 8, p, 4, streams, 5, 0, 2048, p, p, None, 4, p, None) == _native.ERR_MEMBER
+    assert f(0, 3072, 2048, 8, p, 4, streams, 5, 0, 2048, p, p, None, 4, p, None) == _native.ERR_GEOMETRY
+    for start, rows in ((0, 0), (-1, 8), (2040, 16), (0, 2049)):
+        assert f(0, 4096, 2048, 8, p, 4, streams, 5, start, rows, p, p, None, 4, p, None) == _native.ERR_GEOMETRY
+    assert f(0, 4096, 2048, 8, p, 4, streams, 4, 0, 2048, p, p, None, 4, p, None) == _native.ERR_ARGUMENT
+    assert f(1, 4096, 2048, 8, None, 4, streams, 4, 0, 2048, p, p, None, 4, p, None) == _native.ERR_ARGUMENT
+    assert f(1, 4096, 2048, 8, p, 4, streams, 4, 0, 2048, None, p, None, 4, p, None) == _native.ERR_ARGUMENT
+    assert f(1, 4096, 2048, 8, p, 4, streams, 4, 0, 2048, p, p, None, 0, p, None) == _native.OK

@@ -402,3 +402,76 @@ def test_sorted_matmul_range_concat_matches_the_sorted_call(device, member, n):
     narrow = torch.cat([module.sorted_matmul_range(x, idx, 64 + 8 * i, 8) for i in range(2)]
                        + [module.sorted_matmul_range(x, idx, 80, 1)], dim=-1)
     assert np.array_equal(_bits(narrow), _bits(full[..., 64:81]))
+
+
+# -- fused prefill (the producer's weights formed inside the GEMM) ----------
+
+
+def _both_routes(module, *args, **kw):
+    module.fused_prefill = True
+    fused = module(*args, **kw)
+    module.fused_prefill = False
+    producer = module(*args, **kw)
+    module.fused_prefill = True
+    return fused, producer
+
+
+@pytest.mark.parametrize("member", IQ2)
+@pytest.mark.parametrize("n", (2048, 4096))
+def test_fused_prefill_matches_the_producer_route(device, member, n):
+    """Same fp16 weights, f32 sums in another order: the two routes agree to
+    fp16 rounding, and each meets the float64 gate."""
+    print(f"fused prefill {member} n={n}", flush=True)
+    module, ref = _module(member, n, wirepack.seed_for(member, n, "fused"), device)
+    rng = np.random.default_rng(101)
+    tokens, top_k = 40, 4
+    x = rng.standard_normal((tokens, 1, 1, n)).astype(np.float16)
+    idx = np.sort(rng.integers(0, EXPERTS, size=(tokens, top_k)), axis=None).reshape(tokens, top_k).astype(np.int32)
+    xt, it = torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device)
+    fused, producer = _both_routes(module, xt, it, sorted_indices=True)
+    want = oracle.prefill_reference(ref, x, idx)
+    assert _rel(fused, want) < 3e-3 and _rel(producer, want) < 3e-3
+    diff = (fused.float() - producer.float()).abs().max().item()
+    assert diff <= 2e-3 * producer.float().abs().max().item()
+
+
+@pytest.mark.parametrize("member", IQ2)
+@pytest.mark.parametrize("out", (48, 272))
+def test_fused_prefill_serves_partial_row_blocks_and_several_rows_per_pair(device, member, out):
+    """out_features not a multiple of the 256-row block; x [T, M, in] with M = 3
+    rows per pair, unsorted routing over a few experts."""
+    n = 2048
+    module, ref = _module(member, n, 103, device, out=out)
+    rng = np.random.default_rng(107)
+    T, M = 30, 3
+    x = rng.standard_normal((T, M, n)).astype(np.float16)
+    idx = rng.choice([0, 5, 2], size=T).astype(np.int32)
+    fused = module.prefill(torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device))
+    assert tuple(fused.shape) == (T, M, out)
+    want = np.stack([x[t].astype(np.float64) @ ref[idx[t]].astype(np.float64).T for t in range(T)])
+    assert _rel(fused, want) < 3e-3
+
+
+def test_fused_prefill_at_the_routed_geometry(device):
+    """256 experts at the gate/up geometry, a Zipf-skewed 64-token top-6
+    prefill: sampled output rows against float64."""
+    print("fused prefill routed geometry", flush=True)
+    member, E, out, n = "iq2_ks", 256, 2048, 4096
+    wire = wirepack.random_wire(member, E * out, n, seed=2026, scales="serving")
+    shapes = fmt.component_shapes(member, E, out, n)
+    module = IqkSwitchLinear(member, E, out, n, device=device)
+    module.load_streams({k: np.ascontiguousarray(v).reshape(shapes[k])
+                         for k, v in fmt.pack(member, wire, n).items()})
+    rng = np.random.default_rng(9)
+    T, K = 64, 6
+    p = 1.0 / np.arange(1, E + 1) ** 1.1
+    idx = np.stack([rng.choice(E, K, replace=False, p=p / p.sum()) for _ in range(T)]).astype(np.int32)
+    x = rng.standard_normal((T, 1, 1, n)).astype(np.float16)
+    got = module(torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device), sorted_indices=True)
+    got = got.float().cpu().numpy().reshape(T, K, out).astype(np.float64)
+    rows = rng.choice(out, 48, replace=False)
+    for t in range(0, T, 7):
+        for k in range(K):
+            w = oracle.dequantize(member, wire[idx[t, k] * out + rows], n).astype(np.float64)
+            want = w @ x[t, 0, 0].astype(np.float64)
+            assert np.max(np.abs(got[t, k, rows] - want)) / np.max(np.abs(want)) < 3e-3, (t, k)
