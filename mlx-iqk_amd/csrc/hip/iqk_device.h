@@ -68,34 +68,36 @@ struct TileScan {
     uint32_t group, mtile, total;
 };
 
-// The (group, M-tile) of work item t for a 256-thread block: group g of the
+// The (group, M-tile) of work item t for a block of THREADS >= 256 threads
+// (the first 256 scan): group g of the
 // sorted slot ranges [offs[g], offs[g+1]) contributes ceil(size / BM)
 // M-tiles, in group order.  An in-block scan of the group sizes, so a launch
 // needs no host-side knowledge of the routing.  Returns false (uniformly)
 // when t lies beyond the last M-tile.
-template <int BM>
+template <int BM, int THREADS = 256>
 __device__ __forceinline__ bool find_mtile(const uint32_t *offs, uint32_t n_groups, uint32_t t, TileScan &ts,
                                            uint32_t &group, uint32_t &mtile) {
+    static_assert(THREADS >= 256, "the first 256 threads scan");
     const int tid = threadIdx.x;
     if (tid == 0) ts.group = 0xffffffffu;
     uint32_t carry = 0;
     for (uint32_t base = 0; base < n_groups; base += 256) {
         const uint32_t g = base + tid;
         uint32_t cnt = 0;
-        if (g < n_groups) {
+        if (tid < 256 && g < n_groups) {
             const uint32_t c = offs[g + 1] - offs[g];
             cnt = (c + BM - 1) / BM;
         }
         __syncthreads();
-        ts.scan[tid] = cnt;
+        if (tid < 256) ts.scan[tid] = cnt;
         __syncthreads();
         for (int off = 1; off < 256; off <<= 1) {
-            const uint32_t v = tid >= off ? ts.scan[tid - off] : 0u;
+            const uint32_t v = tid >= off && tid < 256 ? ts.scan[tid - off] : 0u;
             __syncthreads();
-            ts.scan[tid] += v;
+            if (tid < 256) ts.scan[tid] += v;
             __syncthreads();
         }
-        const uint32_t incl = carry + ts.scan[tid];
+        const uint32_t incl = carry + (tid < 256 ? ts.scan[tid] : 0u);
         const uint32_t excl = incl - cnt;
         if (cnt && t >= excl && t < incl) {
             ts.group = g;

@@ -19,19 +19,24 @@
 // another (C column blocks), and the activations they share stay in that
 // XCD's L2.
 //
-// Tile: 256 threads, four wavefronts.  Wavefront w owns weight rows
-// 64w .. 64w+63 of the block (four 16-column MFMA blocks j) for all 64 slots
-// (four 16-row MFMA blocks i): 16 accumulators of v_mfma_f32_16x16x32_f16.
-// Reduction steps of 128: lane (n, kg) = (l % 16, l / 16) decodes the 32
-// weights of sub-block kg of the step (k = 128s + 32kg .. +32) of its row and
-// feeds them to the step's four MFMAs t as weights 8t .. 8t+7 (in the order
-// (0,4,1,5,2,6,3,7) that the byte-split table lookup produces; the staged
-// activations are permuted to match).  A lane thus builds its fp16 table once
-// per 32 weights, and the MFMA's k index maps to the same weight for A and B.  The step's activations (64 slots x 128 fp16)
-// are staged in LDS, double buffered, one barrier per step; the code words of
+// Tile: 512 threads, eight wavefronts.  Wavefront w owns weight rows
+// 32w .. 32w+31 of the block (the 32 columns of v_mfma_f32_32x32x16_f16) for
+// all 64 slots (two 32-row MFMA blocks): two 16-register accumulators, so a
+// wavefront needs about 128 VGPRs and four fit per SIMD.
+// Reduction steps of 128: lane (n, kg) = (l % 32, l / 32) decodes the 64
+// weights of sub-blocks 2kg and 2kg+1 of the step (k = 128s + 64kg .. +64)
+// of its row and feeds them to the step's eight MFMAs u as weights
+// 8(u % 4) .. +7 of sub-block 2kg + u / 4, in the order (0,4,1,5,2,6,3,7) that
+// the byte-split table lookup produces; the staged activations are permuted
+// to match.  A lane thus builds its fp16 tables once per sub-block, and the
+// MFMA's k index maps to the same weight for A and B.  The step's
+// activations (64 slots x 128 fp16) are staged in LDS, double buffered, one
+// barrier per step, and read one MFMA operand at a time; the code words of
 // the next step are loaded while this one computes.  The block's scale planes
 // (all 256 rows, whole reduction axis) are copied to LDS once, rows padded so
-// the 16 rows a wavefront reads at once fall in distinct banks.
+// the 32 rows a wavefront reads at once fall in distinct banks.
+
+#include <type_traits>
 
 #include "iqk_device.h"
 #include "iqk_host.h"
@@ -41,9 +46,12 @@ namespace iqk {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 
-constexpr int kFusedBM = 64;    // slots per block
-constexpr int kFusedBN = 256;   // weight rows per block
-constexpr int kFusedKS = 128;   // reduction elements per step
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kFusedBM = 64;        // slots per block
+constexpr int kFusedBN = 256;       // weight rows per block
+constexpr int kFusedKS = 128;       // reduction elements per step
+constexpr int kFusedThreads = 512;  // eight wavefronts of 32 weight rows
 constexpr int kXStride = 2 * kFusedKS + 16;  // LDS bytes per staged activation row
 
 struct FusedArgs {
@@ -83,49 +91,50 @@ __device__ __forceinline__ void copy_plane(const uint8_t *src, int rows, int byt
                                            int tid) {
     const int units_per_row = bytes_per_row / 2;
     const int units = rows * units_per_row;
-    for (int u = tid; u < units; u += 256) {
+    for (int u = tid; u < units; u += kFusedThreads) {
         const int r = u / units_per_row, c = u - r * units_per_row;
         *reinterpret_cast<uint16_t *>(dst + r * stride + 2 * c) = reinterpret_cast<const uint16_t *>(src)[u];
     }
 }
 
-// The two v_perm tables of lane (row, kg) at step s: one per 16-weight word
-// of its 32 weights (IQ2_KS: both from sub-block 4s + kg; IQ2_K: sub-blocks
-// 8s + 2kg and 8s + 2kg + 1).  Same f32 chain as the producer.
+// The v_perm tables of lane (row, kg) at step s, one per 16-weight word of
+// its 64 weights: IQ2_KS sub-blocks 4s + 2kg + h (two words each), IQ2_K
+// sub-blocks 8s + 4kg + w (one word each).  Same f32 chain as the producer.
 template <int MEMBER, int K>
-__device__ __forceinline__ void fused_pools(const FusedScales<MEMBER, K> &sc, int row, int s, int kg, Pool &p0,
-                                            Pool &p1) {
+__device__ __forceinline__ void fused_pools(const FusedScales<MEMBER, K> &sc, int row, int s, int kg, float d,
+                                            Pool *p) {
     using S = FusedScales<MEMBER, K>;
     if constexpr (MEMBER == IQ2_KS) {
-        const int sb = 4 * s + kg;
-        const uint32_t scl = sc.scl[row * S::SCL_S + (sb >> 1)];
-        const uint32_t hb = sc.hb[row * S::HB_S + (sb >> 3)];
-        const uint32_t ab = sc.ex[row * S::EX_S + (sb >> 3)];
-        const uint32_t dvb = *reinterpret_cast<const uint16_t *>(sc.dv + row * S::DV_S);
-        const int idx = int(((scl >> (4 * (sb & 1))) & 15u) | (((hb >> (sb & 7)) & 1u) << 4)) - 16;
-        const bool alpha = (ab >> (sb & 7)) & 1u;
-        const float dl = half_bits_to_float(dvb) * float(idx);
-        p0 = make_pool(dl, alpha ? -26.f : -31.f, alpha ? -8.f : -13.f, alpha ? 6.f : 1.f, alpha ? 22.f : 17.f);
-        p1 = p0;
-    } else {
-        const int sb = 8 * s + 2 * kg;  // first of the lane's two 16-weight sub-blocks
-        const uint32_t scw = *reinterpret_cast<const uint16_t *>(sc.scl + row * S::SCL_S + 2 * (sb >> 2));
-        const uint32_t ab = sc.ex[row * S::EX_S + (sb >> 3)];
-        const uint32_t dvb = *reinterpret_cast<const uint16_t *>(sc.dv + row * S::DV_S + 2 * (sb >> 4));
-        const float d = half_bits_to_float(dvb);
+        const uint32_t scl = sc.scl[row * S::SCL_S + 2 * s + kg];  // nibbles of sub-blocks 4s+2kg, +1
+        const uint32_t hb = sc.hb[row * S::HB_S + (s >> 1)];
+        const uint32_t ab = sc.ex[row * S::EX_S + (s >> 1)];
+        const int bit = 4 * (s & 1) + 2 * kg;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const int idx = int((scw >> (4 * ((sb + h) & 3))) & 15u) - 8;
-            const bool alpha = (ab >> ((sb + h) & 7)) & 1u;
+            const int idx = int(((scl >> (4 * h)) & 15u) | (((hb >> (bit + h)) & 1u) << 4)) - 16;
+            const bool alpha = (ab >> (bit + h)) & 1u;
             const float dl = d * float(idx);
-            (h ? p1 : p0) =
-                make_pool(dl, alpha ? -26.f : -31.f, alpha ? -8.f : -13.f, alpha ? 6.f : 1.f, alpha ? 22.f : 17.f);
+            p[2 * h] = make_pool(dl, alpha ? -26.f : -31.f, alpha ? -8.f : -13.f, alpha ? 6.f : 1.f,
+                                 alpha ? 22.f : 17.f);
+            p[2 * h + 1] = p[2 * h];
+        }
+    } else {
+        const uint32_t scw = *reinterpret_cast<const uint16_t *>(sc.scl + row * S::SCL_S + 2 * (2 * s + kg));
+        const uint32_t ab = sc.ex[row * S::EX_S + s] >> (4 * kg);
+        const float dd = half_bits_to_float(*reinterpret_cast<const uint16_t *>(sc.dv + row * S::DV_S + 2 * (s >> 1)));
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const int idx = int((scw >> (4 * w)) & 15u) - 8;
+            const bool alpha = (ab >> w) & 1u;
+            const float dl = dd * float(idx);
+            p[w] = make_pool(dl, alpha ? -26.f : -31.f, alpha ? -8.f : -13.f, alpha ? 6.f : 1.f,
+                             alpha ? 22.f : 17.f);
         }
     }
 }
 
 template <int MEMBER, int K>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void fused_gemm_kernel(FusedArgs a) {
     using S = FusedScales<MEMBER, K>;
     constexpr int STEPS = K / kFusedKS;
@@ -138,14 +147,12 @@ void fused_gemm_kernel(FusedArgs a) {
     const uint32_t bq = blockIdx.x >> 3, xcd = blockIdx.x & 7u;
     const uint32_t tile = 8 * (bq / ncb) + xcd, cblock = bq % ncb;
     uint32_t g, mtile;
-    if (!find_mtile<kFusedBM>(a.offs, a.n_groups, tile, ts, g, mtile)) return;  // surplus block
+    if (!find_mtile<kFusedBM, kFusedThreads>(a.offs, a.n_groups, tile, ts, g, mtile)) return;  // surplus block
 
     // Offsets and row indices are device data: a slot outside [0, n_slots)
     // is never stored, a row outside x is never read (its output row is 0),
     // and a weight row past out_features is never stored.  Loads of such
-    // rows read an in-bounds row instead, so the step has no branches and the
-    // scheduler can overlap one column block's decode with the MFMAs of the
-    // previous one.
+    // rows read an in-bounds row instead, so the step has no branches.
     const uint32_t gend = min(a.offs[g + 1], a.n_slots);
     const uint32_t m0 = a.offs[g] + mtile * kFusedBM;
     const uint32_t n0 = cblock * kFusedBN;
@@ -163,109 +170,115 @@ void fused_gemm_kernel(FusedArgs a) {
         copy_plane(static_cast<const uint8_t *>(a.s3) + row0 * S::DV, rows_here, S::DV, sc.dv, S::DV_S, tid);
     }
 
-    // activation staging: thread t moves 64 bytes of slot row t/4 per step
-    const int xrow_l = tid >> 2, xseg = tid & 3;
+    // activation staging: thread t moves 32 bytes of slot row t/8 per step
+    const int xrow_l = tid >> 3, xseg = tid & 7;
     const uint32_t xp = m0 + uint32_t(xrow_l);
     const uint32_t xrow = xp < gend ? a.xr[xp] : a.n_x_rows;
     const bool xv = xrow < a.n_x_rows;
-    const uint8_t *xsrc = reinterpret_cast<const uint8_t *>(a.x) + (size_t(xv ? xrow : 0u) * K + 32 * xseg) * 2;
+    const uint8_t *xsrc = reinterpret_cast<const uint8_t *>(a.x) + (size_t(xv ? xrow : 0u) * K + 16 * xseg) * 2;
     const auto load_x = [&](int s, uint4_t *v) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = load_u4(xsrc + 2 * kFusedKS * s + 16 * i);
+        for (int i = 0; i < 2; ++i) v[i] = load_u4(xsrc + 2 * kFusedKS * s + 16 * i);
     };
     // Each 8-element chunk is stored in the order (0,4,1,5,2,6,3,7), the
     // order expand_word_paired gives the weights.
     const auto store_x = [&](int buf, const uint4_t *v) {
-        uint8_t *dst = xs[buf] + xrow_l * kXStride + 64 * xseg;
+        uint8_t *dst = xs[buf] + xrow_l * kXStride + 32 * xseg;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 2; ++i)
             *reinterpret_cast<uint4_t *>(dst + 16 * i) =
                 uint4_t{perm(v[i].z, v[i].x, 0x05040100u), perm(v[i].z, v[i].x, 0x07060302u),
                         perm(v[i].w, v[i].y, 0x05040100u), perm(v[i].w, v[i].y, 0x07060302u)};
     };
 
-    // this lane's weight rows (one per column block j) and code words
-    const int wave = tid >> 6, l = tid & 63, ln = l & 15, kg = l >> 4;
-    int lrow[4];
-    bool wv[4];
-    const uint8_t *qsrc[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        lrow[j] = 64 * wave + 16 * j + ln;
-        wv[j] = lrow[j] < rows_here;
-        qsrc[j] = static_cast<const uint8_t *>(a.s0) + ((row0 + (wv[j] ? lrow[j] : 0)) * (K / 4) + 8 * kg);
-    }
-    const auto load_q = [&](int s, uint2_t *q) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) q[j] = *reinterpret_cast<const uint2_t *>(qsrc[j] + 32 * s);
-    };
+    // this lane's weight row and code words
+    const int wave = tid >> 6, l = tid & 63, ln = l & 31, kg = l >> 5;
+    const int lrow = 32 * wave + ln;
+    const bool wv = lrow < rows_here;
+    const uint8_t *qsrc = static_cast<const uint8_t *>(a.s0) + ((row0 + (wv ? lrow : 0)) * (K / 4) + 16 * kg);
+    const auto load_q = [&](int s) { return load_u4(qsrc + 32 * s); };
 
-    uint4_t xa[4];
-    uint2_t q[4], qn[4];
+    uint4_t xa[2];
     load_x(0, xa);
-    load_q(0, q);
+    uint4_t q = load_q(0), qn;
     store_x(0, xa);
     __syncthreads();  // scale planes and the first activations are in LDS
+    // IQ2_KS row scale (rows past out_features read LDS junk, never stored)
+    const float d = MEMBER == IQ2_KS ? half_bits_to_float(*reinterpret_cast<const uint16_t *>(sc.dv + lrow * S::DV_S))
+                                     : 0.f;
 
-    float4_t acc[4][4];
+    float16_t acc[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int r = 0; r < 16; ++r) acc[mb][r] = 0.f;
 
-    for (int s = 0; s < STEPS; ++s) {
-        const bool more = s + 1 < STEPS;
-        if (more) {
-            load_x(s + 1, xa);
-            load_q(s + 1, qn);
-        }
-        const uint8_t *xb = xs[s & 1];
-        half8_t af[4][4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-                af[i][t] = __builtin_bit_cast(
-                    half8_t, *reinterpret_cast<const uint4_t *>(xb + (16 * i + ln) * kXStride + 64 * kg + 16 * t));
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            uint32_t bw[16];
-            Pool p0, p1;
-            fused_pools<MEMBER, K>(sc, lrow[j], s, kg, p0, p1);  // rows past out_features: LDS junk, never stored
-            expand_word_paired(q[j].x, p0, bw);
-            expand_word_paired(q[j].y, p1, bw + 8);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                // weights 8t .. 8t+7 in the order (0,4,1,5,2,6,3,7)
-                const uint32_t *w8 = bw + 8 * (t >> 1) + (t & 1);
-                const half8_t bf = __builtin_bit_cast(half8_t, uint4_t{w8[0], w8[2], w8[4], w8[6]});
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i][t], bf, acc[i][j], 0, 0, 0);
+    // A tile of at most 32 real slots (most experts of a skewed routing)
+    // runs the second slot block's MFMAs for nothing: skip them.
+    const auto run_steps = [&](auto slot_blocks) {
+        constexpr int MB = decltype(slot_blocks)::value;
+        for (int s = 0; s < STEPS; ++s) {
+            const bool more = s + 1 < STEPS;
+            if (more) {
+                load_x(s + 1, xa);
+                qn = load_q(s + 1);
             }
-        }
-        if (more) {
-            store_x((s + 1) & 1, xa);  // the buffer every wavefront finished reading before the last barrier
+            Pool p[4];
+            fused_pools<MEMBER, K>(sc, lrow, s, kg, d, p);
+            const uint8_t *xb = xs[s & 1] + ln * kXStride + 128 * kg;
+            // A operands of MFMA u (slot blocks 0 .. MB-1)
+            const auto read_a = [&](int u, half8_t *af) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) q[j] = qn[j];
+                for (int mb = 0; mb < MB; ++mb)
+                    af[mb] = __builtin_bit_cast(half8_t, *reinterpret_cast<const uint4_t *>(
+                                                             xb + 32 * mb * kXStride + 64 * (u >> 2) + 16 * (u & 3)));
+            };
+            half8_t af[MB], afn[MB];
+            read_a(0, af);
+            // Word w feeds MFMAs u = 2w, 2w+1 (weights 16(w%2) + 8h .. +7 of
+            // sub-block 2kg + w/2, paired order); expanding word w+1 overlaps
+            // word w's MFMAs.
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                uint32_t bw[8];
+                expand_word_paired(q[w], p[w], bw);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int u = 2 * w + h;
+                    if (u < 7) read_a(u + 1, afn);
+                    const half8_t bf = __builtin_bit_cast(half8_t, uint4_t{bw[h], bw[2 + h], bw[4 + h], bw[6 + h]});
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb) {
+                        acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[mb], bf, acc[mb], 0, 0, 0);
+                        af[mb] = afn[mb];
+                    }
+                }
+            }
+            if (more) {
+                store_x((s + 1) & 1, xa);  // the buffer every wavefront finished reading before the last barrier
+                q = qn;
+            }
+            __syncthreads();
         }
-        __syncthreads();
-    }
+    };
+    if (gend - m0 <= 32)  // uniform per block
+        run_steps(std::integral_constant<int, 1>{});
+    else
+        run_steps(std::integral_constant<int, 2>{});
 
-    // D layout: lane l holds rows 4(l/16) + r of column l % 16.
+    // D layout (32x32): lane l, register r holds row 8(r/4) + 4(l/32) + r%4
+    // of column l % 32.
+    if (!wv) return;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t p = m0 + 16 * i + 4 * kg + r;
-            const bool pv = p < gend;
-            const uint32_t yrow = pv ? (a.yr ? a.yr[p] : p) : a.n_slots;
-            const bool live = pv && a.xr[pv ? p : 0] < a.n_x_rows;  // its activations were real
-            if (yrow < a.n_slots) {
-                uint16_t *yp = a.y + size_t(yrow) * a.N + n0;
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    if (wv[j]) yp[lrow[j]] = live ? uint16_t(float_to_half_bits(acc[i][j][r])) : uint16_t(0);
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t p = m0 + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
+            if (p < gend) {
+                const uint32_t yrow = a.yr ? a.yr[p] : p;
+                const bool live = a.xr[p] < a.n_x_rows;  // its activations were real
+                if (yrow < a.n_slots)
+                    a.y[size_t(yrow) * a.N + n0 + lrow] = live ? uint16_t(float_to_half_bits(acc[mb][r])) : uint16_t(0);
             }
         }
     }
@@ -276,7 +289,7 @@ int launch_fused(int64_t k, const FusedArgs &a, uint32_t n_slots, hipStream_t st
     const uint64_t mtiles = (uint64_t(n_slots) + kFusedBM - 1) / kFusedBM + uint64_t(a.n_groups);
     const uint64_t blocks = (mtiles + 7) / 8 * 8 * ((a.N + kFusedBN - 1) / kFusedBN);
     if (blocks > 0x7fffffffull) return IQK_ERR_ARGUMENT;
-    const dim3 grid{uint32_t(blocks)}, block{256};
+    const dim3 grid{uint32_t(blocks)}, block{kFusedThreads};
     if (k == 4096)
         hipLaunchKernelGGL((fused_gemm_kernel<MEMBER, 4096>), grid, block, 0, st, a);
     else
