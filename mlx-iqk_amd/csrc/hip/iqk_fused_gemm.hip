@@ -48,11 +48,15 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kFusedBM = 64;        // slots per block
-constexpr int kFusedBN = 256;       // weight rows per block
-constexpr int kFusedKS = 128;       // reduction elements per step
-constexpr int kFusedThreads = 512;  // eight wavefronts of 32 weight rows
-constexpr int kXStride = 2 * kFusedKS + 16;  // LDS bytes per staged activation row
+constexpr int kFusedWaves = 8;                   // wavefronts per block, 32 weight rows each
+constexpr int kFusedThreads = 64 * kFusedWaves;
+constexpr int kFusedBM = 64;                     // slots per block
+constexpr int kFusedBN = 32 * kFusedWaves;       // weight rows per block
+constexpr int kFusedKS = 128;                    // reduction elements per step
+constexpr int kXStride = 2 * kFusedKS + 16;      // LDS bytes per staged activation row
+constexpr int kXBytes = kFusedBM * 2 * kFusedKS / kFusedThreads;  // activation bytes a thread stages per step
+constexpr int kXSegs = 2 * kFusedKS / kXBytes;                    // threads per staged row
+static_assert(kXBytes % 16 == 0 && kFusedThreads >= 256, "whole 16-byte chunks; the work-list scan needs 256 threads");
 
 struct FusedArgs {
     const uint16_t *x;
@@ -170,22 +174,22 @@ void fused_gemm_kernel(FusedArgs a) {
         copy_plane(static_cast<const uint8_t *>(a.s3) + row0 * S::DV, rows_here, S::DV, sc.dv, S::DV_S, tid);
     }
 
-    // activation staging: thread t moves 32 bytes of slot row t/8 per step
-    const int xrow_l = tid >> 3, xseg = tid & 7;
+    // activation staging: thread t moves kXBytes of slot row t / kXSegs per step
+    const int xrow_l = tid / kXSegs, xseg = tid % kXSegs;
     const uint32_t xp = m0 + uint32_t(xrow_l);
     const uint32_t xrow = xp < gend ? a.xr[xp] : a.n_x_rows;
     const bool xv = xrow < a.n_x_rows;
-    const uint8_t *xsrc = reinterpret_cast<const uint8_t *>(a.x) + (size_t(xv ? xrow : 0u) * K + 16 * xseg) * 2;
+    const uint8_t *xsrc = reinterpret_cast<const uint8_t *>(a.x) + size_t(xv ? xrow : 0u) * K * 2 + kXBytes * xseg;
     const auto load_x = [&](int s, uint4_t *v) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) v[i] = load_u4(xsrc + 2 * kFusedKS * s + 16 * i);
+        for (int i = 0; i < kXBytes / 16; ++i) v[i] = load_u4(xsrc + 2 * kFusedKS * s + 16 * i);
     };
     // Each 8-element chunk is stored in the order (0,4,1,5,2,6,3,7), the
     // order expand_word_paired gives the weights.
     const auto store_x = [&](int buf, const uint4_t *v) {
-        uint8_t *dst = xs[buf] + xrow_l * kXStride + 32 * xseg;
+        uint8_t *dst = xs[buf] + xrow_l * kXStride + kXBytes * xseg;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < kXBytes / 16; ++i)
             *reinterpret_cast<uint4_t *>(dst + 16 * i) =
                 uint4_t{perm(v[i].z, v[i].x, 0x05040100u), perm(v[i].z, v[i].x, 0x07060302u),
                         perm(v[i].w, v[i].y, 0x05040100u), perm(v[i].w, v[i].y, 0x07060302u)};
@@ -198,7 +202,7 @@ void fused_gemm_kernel(FusedArgs a) {
     const uint8_t *qsrc = static_cast<const uint8_t *>(a.s0) + ((row0 + (wv ? lrow : 0)) * (K / 4) + 16 * kg);
     const auto load_q = [&](int s) { return load_u4(qsrc + 32 * s); };
 
-    uint4_t xa[2];
+    uint4_t xa[kXBytes / 16];
     load_x(0, xa);
     uint4_t q = load_q(0), qn;
     store_x(0, xa);
