@@ -133,6 +133,11 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t grid[MEMBER == IQ1_S_R4 ? IQK_IQ1S_GRID_SIZE : 8];
     __shared__ __attribute__((aligned(16))) uint32_t stage[256 * kStageDwords];
     static_assert(IQK_IQ1S_GRID_SIZE * 2 == 256 * 16, "one 16-byte grid chunk per thread");
+    // IQ1_S_R4's grid load goes out before the stream loads: loads return in
+    // order, so its LDS store and the block barrier below complete while the
+    // stream words are still in flight.
+    uint4_t gridv{};
+    if constexpr (MEMBER == IQ1_S_R4 && !FLOOR) gridv = reinterpret_cast<const uint4_t *>(iqk_iq1s_grid_codes)[threadIdx.x];
     const uint64_t gid = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     const uint64_t lin = gid / TPR;  // (expert, range row)
     const int lc = int(gid % TPR);
@@ -148,9 +153,8 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
         dst = a.w + (uint64_t(slot) * a.rows + r) * N + 64 * lc;
         raw = load_chunk<MEMBER, N>(a, row, lc);
     }
-    if constexpr (MEMBER == IQ1_S_R4 && !FLOOR) {  // the grid, after the stream loads are in flight
-        reinterpret_cast<uint4_t *>(grid)[threadIdx.x] =
-            reinterpret_cast<const uint4_t *>(iqk_iq1s_grid_codes)[threadIdx.x];
+    if constexpr (MEMBER == IQ1_S_R4 && !FLOOR) {
+        reinterpret_cast<uint4_t *>(grid)[threadIdx.x] = gridv;
         __syncthreads();
     }
     if (valid) decode_chunk<MEMBER, FLOOR>(raw, lc, grid, out);
@@ -159,7 +163,13 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
     for (int i = 0; i < 8; ++i)
         reinterpret_cast<uint4_t *>(mine)[i] = uint4_t{out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]};
     *reinterpret_cast<uint64_t *>(mine + 32) = reinterpret_cast<uint64_t>(dst);
-    __syncthreads();
+    // A wavefront's stage is written and read by its own lanes, and LDS
+    // accesses of one wavefront complete in order: a wavefront-scope fence
+    // (ordering for the compiler) replaces a block barrier, so no wavefront
+    // waits for the others of its block.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // chunk c = 64u + l of this wavefront: part c % 8 of its thread c / 8
     const int l = threadIdx.x & 63;
     const uint32_t *wave_stage = stage + (threadIdx.x & ~63) * kStageDwords;
