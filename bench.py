@@ -60,7 +60,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--rounds", type=int, default=5, help="alternated decode/floor rounds per cell")
     ap.add_argument("--block", type=int, default=200, help="dispatches per captured graph in a cell")
     ap.add_argument("--distinct", type=int, default=2, help="distinct quantized experts per projection")
-    ap.add_argument("--cells", default="iq2_ks,iq2_k,iq1_s_r4,dequant,prefill")
+    ap.add_argument("--cells", default="iq2_ks,iq2_k,iq1_s_r4,dequant,prefill,pack")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="CPU baseline sample budget (half on one thread, half on every core)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -379,6 +379,38 @@ def prefill_cell(torch, device, args, seed: int):
     return res
 
 
+def pack_cell(torch, device, args, seed: int):
+    """ik wire -> relayout on the GPU for a 256-expert gate/up stack per member (the
+    on-box ingest of wire already in device memory); GB/s counts bytes read + written."""
+    from mlx_iqk_amd import format as fmt
+    from mlx_iqk_amd import kernels
+
+    res = {}
+    out, n = GU
+    rows = EXPERTS * out
+    for member in ("iq2_ks", "iq2_k", "iq1_s_r4"):
+        rb = fmt.ik_row_bytes(member, n)
+        g = torch.Generator(device=device).manual_seed(seed)
+        wire = torch.randint(0, 256, (rows, rb), dtype=torch.uint8, device=device, generator=g)
+        planes = kernels.pack(member, wire, n)  # warm-up; outputs reused below
+        times = []
+        for _ in range(5):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            kernels.pack(member, wire, n, out=planes)
+            b.record()
+            b.synchronize()
+            times.append(a.elapsed_time(b) * 1e3)
+        us = statistics.median(times)
+        nbytes = 2 * rows * rb
+        res[member] = {"rows": rows, "wire_bytes": rows * rb, "us": round(us, 1),
+                       "gb_per_s": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        log(f"[pack {member}] {rows} rows: {us:.1f} us, {res[member]['gb_per_s']} GB/s (read + written)")
+        del wire, planes
+        torch.cuda.empty_cache()
+    return res
+
+
 # ------------------------------------------------------------------ CPU baseline ---
 
 
@@ -510,6 +542,8 @@ def main() -> int:
         results["dequant"] = {m: dequant_cell(torch, device, m, args, seed=19) for m in ("iq2_ks", "iq2_k", "iq1_s_r4")}
     if "prefill" in cells:
         results["prefill"] = prefill_cell(torch, device, args, seed=23)
+    if "pack" in cells:
+        results["pack"] = pack_cell(torch, device, args, seed=29)
     base = None if args.no_cpu else cpu_baseline(args.cpu_seconds, args.distinct, seed=11)
 
     gu = results["iq2_ks"]["cells"]["gate_up"]

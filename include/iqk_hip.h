@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define IQK_HIP_ABI_VERSION 3
+#define IQK_HIP_ABI_VERSION 4
 
 #define IQK_MEMBER_IQ2_KS 0
 #define IQK_MEMBER_IQ2_K 1
@@ -166,6 +166,16 @@ int iqk_fused_gemm(int member, int64_t in_features, int64_t out_features, int64_
                    int64_t row_start, int64_t rows, const uint32_t *group_offsets,
                    const uint32_t *x_rows, const uint32_t *y_rows, int64_t n_slots,
                    void *y, void *stream);
+
+// ik wire rows -> the member's relayout streams, on the GPU (replaces
+// format.pack for rows already in device memory, src/mlx_iqk/format.py:478-588,
+// 612-678): the bytes pack writes, bit for bit.  wire: u8 [rows, ik row bytes]
+// (4-byte aligned); streams: the member's planes in component order, each
+// [rows, ...] contiguous (qs 16-byte aligned, the others 4-byte aligned).
+// in_features: a multiple of 256 (IQ1_S_R4: of 32); IQ1_S_R4 rows: a multiple
+// of 4 (its four-row groups).
+int iqk_pack(int member, int64_t in_features, int64_t rows, const void *wire,
+             void *const *streams, int n_streams, void *stream);
 
 #ifdef __cplusplus
 }

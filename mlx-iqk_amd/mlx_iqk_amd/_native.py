@@ -12,7 +12,7 @@ from pathlib import Path
 
 from .build import HIP_LIB
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 OK, ERR_MEMBER, ERR_GEOMETRY, ERR_ARGUMENT, ERR_LAUNCH = 0, 1, 2, 3, 4
 _CODES = {ERR_MEMBER: "unknown member", ERR_GEOMETRY: "unsized geometry",
@@ -45,6 +45,7 @@ SIGNATURES = {
                                   c_void_p, c_int64, c_void_p, c_void_p]),
     "iqk_grouped_gemm": (c_int, [c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p,
                                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "iqk_pack": (c_int, [c_int, c_int64, c_int64, c_void_p, ctypes.POINTER(c_void_p), c_int, c_void_p]),
     "iqk_fused_gemm": (c_int, [c_int, c_int64, c_int64, c_int64, c_void_p, c_int64, ctypes.POINTER(c_void_p),
                                c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
 }

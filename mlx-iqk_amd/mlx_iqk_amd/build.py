@@ -35,6 +35,7 @@ HIP_SOURCES = {
     "iqk_dequant.hip": (),
     "iqk_gemm.hip": (),
     "iqk_fused_gemm.hip": (),
+    "iqk_pack.hip": (),
 }
 OFFLOAD_ARCH = "gfx950"
 

@@ -297,6 +297,38 @@ def grouped_gemm(x: torch.Tensor, w: torch.Tensor, group_offsets: torch.Tensor, 
     return out
 
 
+def pack(member: str, wire: torch.Tensor, in_features: int,
+         out: dict[str, torch.Tensor] | None = None) -> dict[str, torch.Tensor]:
+    """``format.pack`` on the GPU: ik wire rows ``u8 [rows, ik_row_bytes]`` already in
+    device memory -> the member's relayout streams (``[rows, ...]`` each), bit for bit.
+    ``out`` may hold the destination planes (e.g. views of a module's buffers)."""
+    from .format import check_wire_rows, ik_row_bytes
+    check_member(member)
+    n = check_row_width(in_features, member)
+    _require_cuda(wire, "wire", torch.uint8)
+    rows = int(wire.shape[0]) if wire.dim() == 2 else -1
+    if wire.dim() != 2 or int(wire.shape[1]) != ik_row_bytes(member, n):
+        raise IqkKernelError(f"{member} wire rows of {n} weights are {ik_row_bytes(member, n)} bytes, "
+                             f"got {tuple(wire.shape)}")
+    check_wire_rows(member, rows)
+    shapes = {k: v[1:] for k, v in component_shapes(member, 1, rows, n).items()}
+    dtypes = stream_dtypes(member)
+    if out is None:
+        out = {k: torch.empty(shape, dtype=dtypes[k], device=wire.device) for k, shape in shapes.items()}
+    else:
+        for k, shape in shapes.items():
+            _require_cuda(out[k], f"stream {k}", dtypes[k], wire.device)
+            if tuple(out[k].shape) != shape:
+                raise IqkKernelError(f"stream {k} must be {shape}, got {tuple(out[k].shape)}")
+    if rows == 0:
+        return out
+    ptrs = _native.pointer_array([out[k].data_ptr() for k in shapes])
+    rc = _native.load().iqk_pack(_native.MEMBER_IDS[member], n, rows, wire.data_ptr(), ptrs, len(shapes),
+                                 _stream_ptr(wire.device))
+    _native.check(rc, f"iqk_pack({member}, {n}, rows={rows})")
+    return out
+
+
 FUSED_MEMBERS = IQ2_MEMBERS
 """Members the fused prefill contraction covers."""
 
@@ -345,6 +377,6 @@ __all__ = [
     "DEQUANT_THREADS", "IQ2_MEMBERS", "MEMBERS", "ROWS_PER_TG",
     "SUPPORTED_IN_FEATURES", "TABLE_INPUT_NAMES", "WEIGHTS_PER_LANE", "IqkKernelError",
     "check_dequant_geometry", "check_gemv_geometry", "check_streams", "dequant", "dequant_input_names",
-    "FUSED_MEMBERS", "check_iq2_member", "fused_matmul", "gemv", "gemv_input_names", "gemv_sorted", "grouped_gemm",
+    "FUSED_MEMBERS", "check_iq2_member", "fused_matmul", "gemv", "pack", "gemv_input_names", "gemv_sorted", "grouped_gemm",
     "stream_dtypes",
 ]

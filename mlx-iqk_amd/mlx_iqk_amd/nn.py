@@ -131,6 +131,19 @@ class IqkSwitchLinear(torch.nn.Module):
         for name, value in staged.items():
             setattr(self, name, value.to(device).contiguous())
 
+    def load_wire(self, wire: torch.Tensor) -> None:
+        """Relayout ik wire rows already on the module's GPU straight into the stream
+        buffers (``format.pack`` + :meth:`load_streams`, on the device).  ``wire`` is
+        ``u8 [num_experts * out_features, ik_row_bytes]``, experts stacked in order."""
+        device = self.qs.device
+        rows = self.num_experts * self.out_features
+        streams = {k: getattr(self, k).view((rows,) + tuple(getattr(self, k).shape[2:])) for k in self.stream_names()}
+        if wire.device != device:
+            raise IqkRuntimeError(f"wire is on {wire.device}, the module on {device}")
+        if wire.dim() != 2 or int(wire.shape[0]) != rows:
+            raise IqkRuntimeError(f"wire must be [{rows}, row bytes], got {tuple(wire.shape)}")
+        kernels.pack(self.member, wire.contiguous(), self.in_features, out=streams)
+
     # -- dequantized route (prefill) -----------------------------------------
 
     def dequantized(self) -> torch.Tensor:

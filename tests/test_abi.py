@@ -127,3 +127,17 @@ def test_fused_gemm_refuses_bad_arguments(lib):
     assert f(1, 4096, 2048, 8, None, 4, streams, 4, 0, 2048, p, p, None, 4, p, None) == _native.ERR_ARGUMENT
     assert f(1, 4096, 2048, 8, p, 4, streams, 4, 0, 2048, None, p, None, 4, p, None) == _native.ERR_ARGUMENT
     assert f(1, 4096, 2048, 8, p, 4, streams, 4, 0, 2048, p, p, None, 0, p, None) == _native.OK
+
+
+def test_pack_refuses_bad_arguments(lib):
+    p = ctypes.c_void_p(16)  # never dereferenced: every call below is refused first
+    streams = _native.pointer_array([16] * 5)
+    f = lib.iqk_pack
+    assert f(3, 2048, 8, p, streams, 5, None) == _native.ERR_MEMBER
+    assert f(0, 2000, 8, p, streams, 5, None) == _native.ERR_GEOMETRY   # not a multiple of 256
+    assert f(2, 2048, 6, p, streams, 3, None) == _native.ERR_GEOMETRY   # IQ1_S_R4 rows in fours
+    assert f(0, 2048, 8, p, streams, 4, None) == _native.ERR_ARGUMENT   # stream count
+    assert f(0, 2048, 8, None, streams, 5, None) == _native.ERR_ARGUMENT
+    assert f(0, 2048, 8, ctypes.c_void_p(18), streams, 5, None) == _native.ERR_ARGUMENT  # wire alignment
+    assert f(0, 2048, 8, p, _native.pointer_array([24] + [16] * 4), 5, None) == _native.ERR_ARGUMENT  # qs alignment
+    assert f(0, 2048, 0, p, streams, 5, None) == _native.OK
