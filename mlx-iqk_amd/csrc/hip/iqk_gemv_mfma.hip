@@ -13,7 +13,10 @@
 //   4-byte pool chosen by the sub-block's alphabet / shift-sign bit.
 //   IQ1_S_R4 looks its eight weights per grid index up in the grid expanded
 //   to int8 (8g + 1) in LDS; the negative shift's 8g - 1 is the exact
-//   correction -2 sum(f) of the block's integer activations.
+//   correction -2 sum(f) of the block's integer activations.  Each workgroup
+//   expands the grid from its 4 KiB of 2-bit codes (a quarter of the bytes
+//   of the expanded grid), each entry's weights in the paired order
+//   0,4,1,5,2,6,3,7, which the staged activations follow.
 // * Activations as integers.  x is converted once per workgroup with a
 //   per-32-element power-of-two scale, f = rint(x * 2^E), |f| <= 2^20, and
 //   split into balanced bytes f = b0 + 2^8 b1 + 2^16 b2 (each b in
@@ -47,7 +50,7 @@
 #include "iqk_device.h"
 #include "iqk_host.h"
 
-#define IQK_GRID_STORAGE static constexpr
+#define IQK_GRID_STORAGE __constant__ static const __attribute__((aligned(16)))
 #include "../iq1s_grid.h"
 
 namespace iqk {
@@ -91,7 +94,6 @@ struct Gemv2Shape {
     static constexpr int THREADS = 64 * 2 * KS;
     static constexpr int UNITS = N / 8;    // activation staging units of 8 elements
     static_assert(THREADS >= UNITS && UNITS % 64 == 0, "whole wavefronts stage the activations");
-    static_assert(IQK_IQ1S_GRID_SIZE / 2 % THREADS == 0, "whole uint4 grid chunks per thread");
 };
 
 // The 16 int8 weights of 16 packed 2-bit codes (code j at bit 2j); operand
@@ -145,25 +147,18 @@ __device__ __forceinline__ void pin(float &v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void pin(uint32_t &v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void pin(int &v) { asm volatile("" : "+v"(v)); }
 
-// IQ1_S_R4's grid expanded to int8 weights 8 * (g + 1/8) = 8g + 1, eight per
-// entry in weight order (two little-endian words), built at compile time from
-// the grid codes (2-bit code c at bit 2k of entry word, g = c - 1).
-struct Iq1B8Table {
-    uint32_t w[2 * IQK_IQ1S_GRID_SIZE];
-};
-
-constexpr Iq1B8Table make_iq1_b8_table() {
-    Iq1B8Table t{};
-    for (int i = 0; i < IQK_IQ1S_GRID_SIZE; ++i)
-        for (int k = 0; k < 8; ++k) {
-            const int c = (iqk_iq1s_grid_codes[i] >> (2 * k)) & 3;
-            const uint32_t b = uint32_t(uint8_t(int8_t(8 * (c - 1) + 1)));
-            t.w[2 * i + k / 4] |= b << (8 * (k % 4));
-        }
-    return t;
+// Two IQ1_S_R4 grid entries (the low and high 16 bits of e; 2-bit code c
+// at bit 2k for weight k, g = c - 1) as int8 weights 8g + 1, eight bytes an
+// entry in the paired order 0,4,1,5,2,6,3,7: word j of the code pattern
+// gathers weights j and 4+j of both entries, one v_perm each from the pool,
+// and two v_perm per 4 bytes regroup them by entry.
+__device__ __forceinline__ void expand_grid_pair(uint32_t e, uint4_t &out) {
+    uint32_t d[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) d[j] = perm(kG8Plus, kG8Plus, (e >> (2 * j)) & 0x03030303u);
+    out = uint4_t{perm(d[1], d[0], 0x05040100u), perm(d[3], d[2], 0x05040100u),   // first entry
+                  perm(d[1], d[0], 0x07060302u), perm(d[3], d[2], 0x07060302u)};  // second entry
 }
-
-__constant__ const Iq1B8Table kIq1B8 = make_iq1_b8_table();
 
 __device__ __forceinline__ int4_t mfma(int4_t a, int4_t b, int4_t c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
@@ -211,27 +206,34 @@ template <int MEMBER>
 constexpr int kExpBlock = MEMBER == IQ2_K ? 64 : 32;
 
 // Activations (fp16) -> balanced byte planes of 16-element words, in the
-// byte order the member's B operand uses.  Thread tid converts 8 activations
-// of word wd, operand dwords 2hp and 2hp+1:
+// byte order the member's B operand uses.  Thread tid = 2wd + hp holds xv,
+// fp16 pairs 4hp..4hp+3 of word wd (its own 16 bytes: each byte of x is
+// loaded once), and converts 8 activations, operand dwords 2hp and 2hp+1:
 //   TRANSPOSED (2-bit members): dword s byte t is element 4t+s, so the
 //     thread takes elements 4t+2hp (low halves) and 4t+2hp+1 (high halves)
-//     of the fp16 pairs 2t+hp;
-//   natural (IQ1_S_R4): dword s byte t is element 4s+t, so the thread takes
-//     elements 8hp..8hp+7, the pairs 4hp..4hp+3.
+//     of the fp16 pairs 2t+hp, two of them from the word's other thread;
+//   paired (IQ1_S_R4): the 8-element group hp holds its elements in the
+//     order 0,4,1,5,2,6,3,7 of the grid expansion, so the thread takes
+//     elements 8hp..8hp+7, the pairs 4hp..4hp+3 it holds.
 // One exponent E covers BLOCK (32 or 64) consecutive elements, 2^-E lands in
 // sbs[element / BLOCK].  With `fsum` / `fword`, each 32-element block's /
 // 16-element word's sum(f) lands there too; with ZERO_SPAN, the WK bytes
 // after the planes are cleared.
 template <int N, bool TRANSPOSED, bool ZERO_SPAN, int BLOCK, int WK>
 __device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, int *fsum, float *fword, int tid,
-                                                  uint4_t x0, uint4_t x1) {
+                                                  uint4_t xv) {
     static_assert(BLOCK == 32 || BLOCK == 64, "4 or 8 threads per exponent block");
     const uint32_t wd = uint32_t(tid) >> 1, hp = uint32_t(tid) & 1u;
     if (ZERO_SPAN && tid < WK / 16)
         *reinterpret_cast<uint4_t *>(dig + 3 * kPlaneStride<N> + 16 * tid) = uint4_t{0u, 0u, 0u, 0u};
-    const uint4_t xv = hp ? x1 : x0;
-    const uint32_t xp[4] = {TRANSPOSED ? (hp ? x0.y : x0.x) : xv.x, TRANSPOSED ? (hp ? x0.w : x0.z) : xv.y,
-                            TRANSPOSED ? (hp ? x1.y : x1.x) : xv.z, TRANSPOSED ? (hp ? x1.w : x1.z) : xv.w};
+    uint32_t xp[4] = {xv.x, xv.y, xv.z, xv.w};
+    if constexpr (TRANSPOSED) {  // hp 0 keeps pairs 0, 2 and takes 4, 6; hp 1 keeps 5, 7 and takes 1, 3
+        const uint32_t r0 = quad_xor<1>(hp ? xv.x : xv.y), r1 = quad_xor<1>(hp ? xv.z : xv.w);
+        xp[0] = hp ? r0 : xv.x;
+        xp[1] = hp ? r1 : xv.z;
+        xp[2] = hp ? xv.y : r0;
+        xp[3] = hp ? xv.w : r1;
+    }
     // max |x| on the fp16 bits (magnitude order is integer order)
     ushort2_t m2 = __builtin_bit_cast(ushort2_t, xp[0] & 0x7fff7fffu);
 #pragma unroll
@@ -265,10 +267,10 @@ __device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, int 
         if constexpr (TRANSPOSED) {
             u0[t] = blo[t];
             u1[t] = bhi[t];
-        } else {
-            const int e = 2 * (t & 1);
-            (t < 2 ? u0 : u1)[e] = blo[t];
-            (t < 2 ? u0 : u1)[e + 1] = bhi[t];
+        } else {  // elements 2t, 2t+1 at positions 2(2t % 4) + 2t / 4 and that + 2
+            const int pos = 4 * (t & 1) + (t >> 1);
+            (pos < 4 ? u0 : u1)[pos & 3] = blo[t];
+            (pos < 4 ? u0 : u1)[(pos & 3) + 2] = bhi[t];
         }
     }
     if (fsum || fword) {  // sums of f (mod 2^32, exact: |sum| < 2^26)
@@ -587,25 +589,20 @@ void gemv_mfma_kernel(Gemv2Args a) {
     // expert id, and vector loads retire in order, so staging them waits for
     // none of the stream bytes issued after them.
     const bool stager = tid < S::UNITS;  // uniform per wavefront
-    const auto load_x = [&](uint32_t tok, uint4_t &x0, uint4_t &x1) {
-        const uint32_t xo = tok * (2 * N) + 32 * (uint32_t(tid) >> 1);
-        x0 = uint4_t{0u, 0u, 0u, 0u};
-        x1 = uint4_t{0u, 0u, 0u, 0u};
-        if (stager) {
-            x0 = load_u4(bytes(a.x) + xo);
-            x1 = load_u4(bytes(a.x) + (xo + 16));
-        }
+    const auto load_x = [&](uint32_t tok, uint4_t &xv) {  // fp16 pairs 4tid .. 4tid+3 of row tok
+        xv = uint4_t{0u, 0u, 0u, 0u};
+        if (stager) xv = load_u4(bytes(a.x) + (tok * (2 * N) + 16 * uint32_t(tid)));
     };
     uint32_t tok = x_row(m0);
     bool x_ok = MODE == kPairs || tok < a.n_x_rows;
-    uint4_t x0, x1;
-    load_x(x_ok ? tok : 0u, x0, x1);
+    uint4_t xv;
+    load_x(x_ok ? tok : 0u, xv);
     constexpr bool IQ1 = MEMBER == IQ1_S_R4;
-    constexpr int GRID_CHUNKS = IQ1 && !FLOOR ? IQK_IQ1S_GRID_SIZE / 2 / S::THREADS : 0;  // uint4 per thread
-    uint4_t gridv[GRID_CHUNKS > 0 ? GRID_CHUNKS : 1];
-#pragma unroll
-    for (int i = 0; i < GRID_CHUNKS; ++i)
-        gridv[i] = reinterpret_cast<const uint4_t *>(kIq1B8.w)[tid + i * S::THREADS];
+    // IQ1_S_R4: the codes of grid entries 4tid .. 4tid+3
+    constexpr bool GRID = IQ1 && !FLOOR;
+    static_assert(!IQ1 || IQK_IQ1S_GRID_SIZE == 4 * S::THREADS, "four grid entries per thread");
+    uint2_t gridc = {0u, 0u};
+    if constexpr (GRID) gridc = reinterpret_cast<const uint2_t *>(iqk_iq1s_grid_codes)[tid];
     constexpr bool KTAB = MEMBER == IQ2_K && !FLOOR;
     uint2_t ktv = {0u, 0u};
     if (KTAB && tid < 32) ktv = reinterpret_cast<const uint2_t *>(kIq2kTab.w)[tid];
@@ -627,23 +624,26 @@ void gemv_mfma_kernel(Gemv2Args a) {
         if (q > 0) {  // kUnion: the run's next pair, same stream registers
             tok = x_row(m);
             x_ok = tok < a.n_x_rows;
-            load_x(x_ok ? tok : 0u, x0, x1);
+            load_x(x_ok ? tok : 0u, xv);
         }
         float acc;
         if constexpr (FLOOR) {
-            const uint32_t h = x0.x + 3u * x0.y + 5u * x0.z + 7u * x0.w + 11u * x1.x + 13u * x1.y + 17u * x1.z +
-                               19u * x1.w + lane.hash();
+            const uint32_t h = xv.x + 3u * xv.y + 5u * xv.z + 7u * xv.w + lane.hash();
             acc = float(h & 0xffu);
         } else {
             if (q == 0) {
-#pragma unroll
-                for (int i = 0; i < GRID_CHUNKS; ++i)
-                    reinterpret_cast<uint4_t *>(sm.b8)[tid + i * S::THREADS] = gridv[i];
+                if constexpr (GRID) {
+                    uint4_t g0, g1;
+                    expand_grid_pair(gridc.x, g0);
+                    expand_grid_pair(gridc.y, g1);
+                    reinterpret_cast<uint4_t *>(sm.b8)[2 * tid] = g0;
+                    reinterpret_cast<uint4_t *>(sm.b8)[2 * tid + 1] = g1;
+                }
                 if (KTAB && tid < 32) sm.ktab[tid] = ktv;
             }
             if (stager)
                 stage_activations<N, !IQ1, !kMaskedA<MEMBER>, kExpBlock<MEMBER>, S::WK>(
-                    sm.dig, sm.sbs, IQ1 ? sm.fsum : nullptr, MEMBER == IQ2_K ? sm.fw : nullptr, tid, x0, x1);
+                    sm.dig, sm.sbs, IQ1 ? sm.fsum : nullptr, MEMBER == IQ2_K ? sm.fw : nullptr, tid, xv);
             __syncthreads();
             const int ai = l & 15;  // this lane's A row
             const bool data = (ai >> 2) == g && (ai & 3) < 3;
