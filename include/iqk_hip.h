@@ -159,8 +159,7 @@ int iqk_grouped_gemm(int64_t in_features, int64_t out_features, int64_t n_groups
 // concatenate to the full call bit for bit).  y: f16 [n_slots, rows];
 // group_offsets: u32 [num_experts + 1] (device, non-decreasing, last =
 // n_slots); x, x_rows, y_rows as iqk_grouped_gemm.  IQK_ERR_GEOMETRY unless
-// 0 <= row_start < row_start + rows <= out_features.  IQK_MEMBER_IQ2_KS and
-// IQK_MEMBER_IQ2_K; IQ1_S_R4 returns IQK_ERR_MEMBER.
+// 0 <= row_start < row_start + rows <= out_features.  All three members.
 int iqk_fused_gemm(int member, int64_t in_features, int64_t out_features, int64_t num_experts,
                    const void *x, int64_t n_x_rows, const void *const *streams, int n_streams,
                    int64_t row_start, int64_t rows, const uint32_t *group_offsets,

@@ -35,12 +35,21 @@
 // the next step are loaded while this one computes.  The block's scale planes
 // (all 256 rows, whole reduction axis) are copied to LDS once, rows padded so
 // the 32 rows a wavefront reads at once fall in distinct banks.
+//
+// IQ1_S_R4: the lane's two 32-weight blocks of a step bring their index bytes
+// and qh words with the step's loads (no scale planes), and the block's 4 KiB
+// of grid codes sit in LDS; two grid entries make one 16-code word, expanded
+// with the producer's pool of the block, so the weights are again the
+// producer's.
 
 #include <type_traits>
 
 #include "iqk_device.h"
 #include "iqk_host.h"
 #include "iqk_pool.h"
+
+#define IQK_GRID_STORAGE __constant__ static const __attribute__((aligned(16)))
+#include "../iq1s_grid.h"
 
 namespace iqk {
 
@@ -137,14 +146,39 @@ __device__ __forceinline__ void fused_pools(const FusedScales<MEMBER, K> &sc, in
     }
 }
 
+// IQ1_S_R4 at one step: blocks b = 0, 1 of the lane (index bytes q[b], qh
+// word b of q.z).  Pools p[2b], p[2b+1] are block b's (dl = d (2s+1), values
+// g + shift, as the producer), and word 2b+t holds the grid codes of the
+// block's 8-weight groups 2t and 2t+1.
+__device__ __forceinline__ void fused_iq1(uint4_t q, const uint16_t *grid, float d, Pool *p, uint32_t *words) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const uint32_t qw = q[b], h = (q.z >> (16 * b)) & 0xffffu;
+        const float dl = d * float(int(2 * ((h >> 12) & 7u) + 1));
+        const float sh = (h & 0x8000u) ? -0.125f : 0.125f;
+        p[2 * b] = make_pool(dl, -1.f + sh, 0.f + sh, 1.f + sh, 2.f + sh);  // grid field 3 never occurs
+        p[2 * b + 1] = p[2 * b];
+        uint32_t c[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) c[t] = grid[((qw >> (8 * t)) & 0xffu) | (((h >> (3 * t)) & 7u) << 8)];
+        words[2 * b] = c[0] | (c[1] << 16);
+        words[2 * b + 1] = c[2] | (c[3] << 16);
+    }
+}
+
+struct FusedGrid {
+    uint16_t codes[IQK_IQ1S_GRID_SIZE];
+};
+
 template <int MEMBER, int K>
 __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void fused_gemm_kernel(FusedArgs a) {
-    using S = FusedScales<MEMBER, K>;
+    constexpr bool IQ1 = MEMBER == IQ1_S_R4;
+    using S = FusedScales<IQ1 ? IQ2_KS : MEMBER, K>;
     constexpr int STEPS = K / kFusedKS;
     __shared__ TileScan ts;
     __shared__ __attribute__((aligned(16))) uint8_t xs[2][kFusedBM * kXStride];
-    __shared__ __attribute__((aligned(16))) S sc;
+    __shared__ __attribute__((aligned(16))) std::conditional_t<IQ1, FusedGrid, S> sc;
 
     const int tid = threadIdx.x;
     const uint32_t ncb = (a.N + kFusedBN - 1) / kFusedBN;  // column blocks
@@ -163,13 +197,19 @@ void fused_gemm_kernel(FusedArgs a) {
     const int rows_here = int(min(uint32_t(kFusedBN), a.N - n0));
     const size_t row0 = size_t(g) * a.out_rows + a.row_start + n0;  // first stacked weight row of the block
 
-    // scale planes of the block's rows
-    copy_plane(static_cast<const uint8_t *>(a.s1) + row0 * S::SCL, rows_here, S::SCL, sc.scl, S::SCL_S, tid);
+    // scale planes of the block's rows (IQ1_S_R4: the grid codes)
+    if constexpr (IQ1) {
+        static_assert(IQK_IQ1S_GRID_SIZE * 2 / 16 <= kFusedThreads, "one 16-byte chunk of the grid per thread");
+        if (tid < IQK_IQ1S_GRID_SIZE * 2 / 16)
+            reinterpret_cast<uint4_t *>(sc.codes)[tid] = reinterpret_cast<const uint4_t *>(iqk_iq1s_grid_codes)[tid];
+    } else {
+        copy_plane(static_cast<const uint8_t *>(a.s1) + row0 * S::SCL, rows_here, S::SCL, sc.scl, S::SCL_S, tid);
+    }
     if constexpr (MEMBER == IQ2_KS) {
         copy_plane(static_cast<const uint8_t *>(a.s2) + row0 * S::HB, rows_here, S::HB, sc.hb, S::HB_S, tid);
         copy_plane(static_cast<const uint8_t *>(a.s3) + row0 * S::EX, rows_here, S::EX, sc.ex, S::EX_S, tid);
         copy_plane(static_cast<const uint8_t *>(a.s4) + row0 * S::DV, rows_here, S::DV, sc.dv, S::DV_S, tid);
-    } else {
+    } else if constexpr (MEMBER == IQ2_K) {
         copy_plane(static_cast<const uint8_t *>(a.s2) + row0 * S::EX, rows_here, S::EX, sc.ex, S::EX_S, tid);
         copy_plane(static_cast<const uint8_t *>(a.s3) + row0 * S::DV, rows_here, S::DV, sc.dv, S::DV_S, tid);
     }
@@ -199,17 +239,33 @@ void fused_gemm_kernel(FusedArgs a) {
     const int wave = tid >> 6, l = tid & 63, ln = l & 31, kg = l >> 5;
     const int lrow = 32 * wave + ln;
     const bool wv = lrow < rows_here;
-    const uint8_t *qsrc = static_cast<const uint8_t *>(a.s0) + ((row0 + (wv ? lrow : 0)) * (K / 4) + 16 * kg);
-    const auto load_q = [&](int s) { return load_u4(qsrc + 32 * s); };
+    const size_t wrow = row0 + (wv ? lrow : 0);  // in-bounds row for the loads
+    // IQ2 members: the step's four code words; IQ1_S_R4: the two blocks'
+    // index words and their qh words (blocks 4s + 2kg, +1)
+    const uint8_t *qsrc = static_cast<const uint8_t *>(a.s0) + (IQ1 ? wrow * (K / 8) + 8 * kg : wrow * (K / 4) + 16 * kg);
+    const uint8_t *hsrc = static_cast<const uint8_t *>(a.s1) + (wrow * (K / 16) + 4 * kg);
+    const auto load_q = [&](int s) {
+        if constexpr (IQ1) {
+            const uint2_t iw = *reinterpret_cast<const uint2_t *>(qsrc + 16 * s);
+            return uint4_t{iw.x, iw.y, *reinterpret_cast<const uint32_t *>(hsrc + 8 * s), 0u};
+        } else {
+            return load_u4(qsrc + 32 * s);
+        }
+    };
 
     uint4_t xa[kXBytes / 16];
     load_x(0, xa);
     uint4_t q = load_q(0), qn;
     store_x(0, xa);
     __syncthreads();  // scale planes and the first activations are in LDS
-    // IQ2_KS row scale (rows past out_features read LDS junk, never stored)
-    const float d = MEMBER == IQ2_KS ? half_bits_to_float(*reinterpret_cast<const uint16_t *>(sc.dv + lrow * S::DV_S))
-                                     : 0.f;
+    // row scale: IQ2_KS from LDS (rows past out_features read LDS junk, never
+    // stored), IQ1_S_R4 from its stream (an in-bounds row); IQ2_K's are per
+    // super-block
+    float d = 0.f;
+    if constexpr (MEMBER == IQ2_KS)
+        d = half_bits_to_float(*reinterpret_cast<const uint16_t *>(sc.dv + lrow * S::DV_S));
+    else if constexpr (IQ1)
+        d = half_bits_to_float(static_cast<const uint16_t *>(a.s2)[wrow]);
 
     float16_t acc[2];
 #pragma unroll
@@ -228,7 +284,14 @@ void fused_gemm_kernel(FusedArgs a) {
                 qn = load_q(s + 1);
             }
             Pool p[4];
-            fused_pools<MEMBER, K>(sc, lrow, s, kg, d, p);
+            uint32_t words[4];
+            if constexpr (IQ1) {
+                fused_iq1(q, sc.codes, d, p, words);
+            } else {
+                fused_pools<MEMBER, K>(sc, lrow, s, kg, d, p);
+#pragma unroll
+                for (int w = 0; w < 4; ++w) words[w] = q[w];
+            }
             const uint8_t *xb = xs[s & 1] + ln * kXStride + 128 * kg;
             // A operands of MFMA u (slot blocks 0 .. MB-1)
             const auto read_a = [&](int u, half8_t *af) {
@@ -245,7 +308,7 @@ void fused_gemm_kernel(FusedArgs a) {
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
                 uint32_t bw[8];
-                expand_word_paired(q[w], p[w], bw);
+                expand_word_paired(words[w], p[w], bw);
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int u = 2 * w + h;
@@ -310,7 +373,6 @@ extern "C" int iqk_fused_gemm(int member, int64_t in_features, int64_t out_featu
                               void *stream) {
     using namespace iqk;
     if (!member_ok(member)) return IQK_ERR_MEMBER;
-    if (member == IQK_MEMBER_IQ1_S_R4) return IQK_ERR_MEMBER;  // no fused form (yet): producer + grouped GEMM
     if (!width_sized(in_features)) return IQK_ERR_GEOMETRY;
     if (out_features <= 0 || out_features > (int64_t(1) << 24)) return IQK_ERR_GEOMETRY;
     if (row_start < 0 || rows <= 0 || row_start + rows > out_features) return IQK_ERR_GEOMETRY;
@@ -321,7 +383,8 @@ extern "C" int iqk_fused_gemm(int member, int64_t in_features, int64_t out_featu
     if (!x || !y || !group_offsets || !x_rows || !streams_ok(streams, n_streams, member)) return IQK_ERR_ARGUMENT;
     FusedArgs a;
     a.x = static_cast<const uint16_t *>(x);
-    a.s0 = streams[0]; a.s1 = streams[1]; a.s2 = streams[2]; a.s3 = streams[3];
+    a.s0 = streams[0]; a.s1 = streams[1]; a.s2 = streams[2];
+    a.s3 = n_streams > 3 ? streams[3] : nullptr;
     a.s4 = n_streams > 4 ? streams[4] : nullptr;
     a.offs = group_offsets;
     a.xr = x_rows;
@@ -334,6 +397,9 @@ extern "C" int iqk_fused_gemm(int member, int64_t in_features, int64_t out_featu
     a.n_slots = uint32_t(n_slots);
     a.n_x_rows = uint32_t(n_x_rows);
     hipStream_t st = as_stream(stream);
-    return member == IQK_MEMBER_IQ2_KS ? launch_fused<IQ2_KS>(in_features, a, uint32_t(n_slots), st)
-                                       : launch_fused<IQ2_K>(in_features, a, uint32_t(n_slots), st);
+    switch (member) {
+        case IQK_MEMBER_IQ2_KS: return launch_fused<IQ2_KS>(in_features, a, uint32_t(n_slots), st);
+        case IQK_MEMBER_IQ2_K: return launch_fused<IQ2_K>(in_features, a, uint32_t(n_slots), st);
+        default: return launch_fused<IQ1_S_R4>(in_features, a, uint32_t(n_slots), st);
+    }
 }

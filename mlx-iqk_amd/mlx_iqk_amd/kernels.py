@@ -329,8 +329,8 @@ def pack(member: str, wire: torch.Tensor, in_features: int,
     return out
 
 
-FUSED_MEMBERS = IQ2_MEMBERS
-"""Members the fused prefill contraction covers."""
+FUSED_MEMBERS = MEMBERS
+"""Members the fused prefill contraction covers (all three)."""
 
 
 def fused_matmul(member: str, x: torch.Tensor, streams: list[torch.Tensor], num_experts: int, out_features: int,

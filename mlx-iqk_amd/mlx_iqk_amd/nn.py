@@ -75,9 +75,9 @@ class IqkSwitchLinear(torch.nn.Module):
 
     mode = "iqk"
     fused_prefill = True
-    """Prefill through the fused contraction (IQ2 members: the producer's fp16
-    weights formed inside the GEMM, never stored) rather than producer + grouped
-    GEMM.  Both give the same weights; the f32 summation order differs."""
+    """Prefill through the fused contraction (the producer's fp16 weights
+    formed inside the GEMM, never stored) rather than producer + grouped GEMM.
+    Both give the same weights; the f32 summation order differs."""
 
     def __init__(self, member: str, num_experts: int, out_features: int, in_features: int,
                  device=None):

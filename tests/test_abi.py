@@ -118,7 +118,7 @@ def test_fused_gemm_refuses_bad_arguments(lib):
     p = ctypes.c_void_p(16)  # never dereferenced: every call below is refused first
     streams = _native.pointer_array([16] * 5)
     f = lib.iqk_fused_gemm
-    assert f(2, 4096, 2048, 8, p, 4, streams, 3, 0, 2048, p, p, None, 4, p, None) == _native.ERR_MEMBER
+    assert f(2, 4096, 2048, 8, p, 4, streams, 5, 0, 2048, p, p, None, 4, p, None) == _native.ERR_ARGUMENT
     assert f(7, 4096, 2048, 8, p, 4, streams, 5, 0, 2048, p, p, None, 4, p, None) == _native.ERR_MEMBER
     assert f(0, 3072, 2048, 8, p, 4, streams, 5, 0, 2048, p, p, None, 4, p, None) == _native.ERR_GEOMETRY
     for start, rows in ((0, 0), (-1, 8), (2040, 16), (0, 2049)):

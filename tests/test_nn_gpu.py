@@ -416,7 +416,7 @@ def _both_routes(module, *args, **kw):
     return fused, producer
 
 
-@pytest.mark.parametrize("member", IQ2)
+@pytest.mark.parametrize("member", fmt.MEMBERS)
 @pytest.mark.parametrize("n", (2048, 4096))
 def test_fused_prefill_matches_the_producer_route(device, member, n):
     """Same fp16 weights, f32 sums in another order: the two routes agree to
@@ -435,7 +435,7 @@ def test_fused_prefill_matches_the_producer_route(device, member, n):
     assert diff <= 2e-3 * producer.float().abs().max().item()
 
 
-@pytest.mark.parametrize("member", IQ2)
+@pytest.mark.parametrize("member", fmt.MEMBERS)
 @pytest.mark.parametrize("out", (48, 272))
 def test_fused_prefill_serves_partial_row_blocks_and_several_rows_per_pair(device, member, out):
     """out_features not a multiple of the 256-row block; x [T, M, in] with M = 3
@@ -452,11 +452,12 @@ def test_fused_prefill_serves_partial_row_blocks_and_several_rows_per_pair(devic
     assert _rel(fused, want) < 3e-3
 
 
-def test_fused_prefill_at_the_routed_geometry(device):
+@pytest.mark.parametrize("member", ("iq2_ks", "iq1_s_r4"))
+def test_fused_prefill_at_the_routed_geometry(device, member):
     """256 experts at the gate/up geometry, a Zipf-skewed 64-token top-6
     prefill: sampled output rows against float64."""
-    print("fused prefill routed geometry", flush=True)
-    member, E, out, n = "iq2_ks", 256, 2048, 4096
+    print(f"fused prefill routed geometry {member}", flush=True)
+    E, out, n = 256, 2048, 4096
     wire = wirepack.random_wire(member, E * out, n, seed=2026, scales="serving")
     shapes = fmt.component_shapes(member, E, out, n)
     module = IqkSwitchLinear(member, E, out, n, device=device)
@@ -469,7 +470,8 @@ def test_fused_prefill_at_the_routed_geometry(device):
     x = rng.standard_normal((T, 1, 1, n)).astype(np.float16)
     got = module(torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device), sorted_indices=True)
     got = got.float().cpu().numpy().reshape(T, K, out).astype(np.float64)
-    rows = rng.choice(out, 48, replace=False)
+    # whole four-row groups: IQ1_S_R4's wire interleaves the rows of a group
+    rows = (4 * rng.choice(out // 4, 12, replace=False)[:, None] + np.arange(4)).reshape(-1)
     for t in range(0, T, 7):
         for k in range(K):
             w = oracle.dequantize(member, wire[idx[t, k] * out + rows], n).astype(np.float64)
