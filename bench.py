@@ -283,7 +283,8 @@ def dequant_cell(torch, device, member: str, args, seed: int):
 
 
 def prefill_cell(torch, device, args, seed: int):
-    """2048 tokens, Zipf(1.1) top-6 sorted routing; gate/up IQ2_KS, down IQ2_K."""
+    """2048 tokens, Zipf(1.1) top-6 sorted routing; gate/up IQ2_KS, down IQ2_K (the
+    totals), and the gate projection once more as IQ1_S_R4 (reported beside them)."""
     from mlx_iqk_amd import format as fmt
     from mlx_iqk_amd import kernels, synth
     from mlx_iqk_amd.nn import IqkSwitchLinear
@@ -297,7 +298,8 @@ def prefill_cell(torch, device, args, seed: int):
     x = torch.randn(flat.size, 1, GU[1], device=device).to(torch.float16)
     h = torch.randn(flat.size, 1, DN[1], device=device).to(torch.float16)
     ids = torch.from_numpy(flat.astype(np.int32)).to(device)
-    projections = (("gate", "iq2_ks", GU, x), ("up", "iq2_ks", GU, x), ("down", "iq2_k", DN, h))
+    projections = (("gate", "iq2_ks", GU, x), ("up", "iq2_ks", GU, x), ("down", "iq2_k", DN, h),
+                   ("gate_iq1_s_r4", "iq1_s_r4", GU, x))
     res = {"tokens": tokens, "pairs": int(flat.size), "experts_routed": int((counts > 0).sum()),
            "max_pairs_per_expert": int(counts.max()), "projections": {}}
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
@@ -361,16 +363,18 @@ def prefill_cell(torch, device, args, seed: int):
                   "fused_max_dev_vs_producer_route": round(fused_dev, 6)})
         r["fused_mfma_utilisation"] = round(r["fused_tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
         res["projections"][name] = r
-        tot_fused += med["fused"]
-        tot_prod += med["producer"]
-        tot_gemm += med["gemm"]
-        tot_bytes += nbytes
-        tot_flop += flop
         log(f"  {name}: producer {med['producer']:.1f} us ({r['producer_gb_per_s']} GB/s, x{r['producer_x_floor']})"
             f"  gemm {med['gemm']:.1f} us ({r['gemm_tflops']} TFLOP/s)"
             f"  fused {med['fused']:.1f} us ({r['fused_tflops']} TFLOP/s, dev {fused_dev:.2e})")
         del mod, w, y, yf, yp
         torch.cuda.empty_cache()
+        if member == "iq1_s_r4":  # outside the prefill configuration's totals
+            continue
+        tot_fused += med["fused"]
+        tot_prod += med["producer"]
+        tot_gemm += med["gemm"]
+        tot_bytes += nbytes
+        tot_flop += flop
     res["producer_gb_per_s"] = round(tot_bytes / (tot_prod * 1e-6) / 1e9, 1)
     res["gemm_tflops"] = round(tot_flop / (tot_gemm * 1e-6) / 1e12, 2)
     res["mfma_utilisation"] = round(res["gemm_tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
