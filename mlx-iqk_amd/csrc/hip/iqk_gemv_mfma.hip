@@ -396,11 +396,12 @@ struct LaneIq2k {
     // activation sum fw.  A lane folds once per super-block.
     __device__ __forceinline__ float decode(const uint8_t *abase, const float *sbs, const float *fw,
                                             const uint2_t *ktab, int g) const {
-        // this lane's scale word of super-block s: u16 4s+g of the wavefront's 16
-        const bool gh = (g >> 1) != 0;
-        const int sh16 = 16 * (g & 1);
-        const uint32_t scw[4] = {(gh ? sc0.y : sc0.x) >> sh16, (gh ? sc0.w : sc0.z) >> sh16,
-                                 (gh ? sc1.y : sc1.x) >> sh16, (gh ? sc1.w : sc1.z) >> sh16};
+        // This lane's scale word of super-block s is u16 g of the pair
+        // (sc.y:sc.x) or (sc.w:sc.z); one v_perm spreads its two bytes to
+        // (b0, b0, b1, b1), and shifts put nibble j at bits 3-6 of byte j.
+        const uint32_t selg = 0x01010000u + uint32_t(2 * g) * 0x01010101u;
+        const uint32_t scp[4] = {perm(sc0.y, sc0.x, selg), perm(sc0.w, sc0.z, selg), perm(sc1.y, sc1.x, selg),
+                                 perm(sc1.w, sc1.z, selg)};
         // alphabet bits of super-block s: byte 2s + g/2 of ex, bits 4(g%2) + j
         const int exs = 8 * (g >> 1) + 4 * (g & 1);
         const uint32_t exg[2] = {ex.x >> exs, ex.y >> exs};
@@ -413,11 +414,18 @@ struct LaneIq2k {
             const float4 fwv = *reinterpret_cast<const float4 *>(fw + 16 * s + 4 * g);
             dfac[s] = half_bits_to_float((dv[s >> 1] >> (16 * (s & 1))) & 0xffffu) * sbs[4 * s + g];
             offs[s] = 0.f;
+            // byte j: the table's byte offset 8 (alpha_j << 4 | nib_j) of word
+            // j; the multiply copies alphabet bit j to bit 8j (no two copies
+            // meet, so no carries; pinned, or it becomes a quarter-rate
+            // 32-bit multiply by the shifted constant)
+            uint32_t a8 = __umul24((exg[s >> 1] >> (16 * (s & 1))) & 15u, 0x204081u);
+            pin(a8);
+            const uint32_t kofs = ((scp[s] << 3) & 0x00780078u) | ((scp[s] >> 1) & 0x78007800u) |
+                                  ((a8 & 0x01010101u) << 7);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const uint32_t nib = (scw[s] >> (4 * j)) & 15u;
-                const uint32_t alpha = (exg[s >> 1] >> (16 * (s & 1) + j)) & 1u;
-                const uint2_t e = ktab[alpha * 16 + nib];
+                const uint2_t e = *reinterpret_cast<const uint2_t *>(reinterpret_cast<const uint8_t *>(ktab) +
+                                                                     ((kofs >> (8 * j)) & 0xffu));
                 pools[s][j] = e.x;
                 offs[s] = fmaf(__uint_as_float(e.y), fwv[j], offs[s]);
             }
