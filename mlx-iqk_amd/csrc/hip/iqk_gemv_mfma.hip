@@ -107,12 +107,6 @@ __device__ __forceinline__ int4_t codes_to_i8(uint32_t q, uint32_t pool) {
     return b;
 }
 
-// pool_b if bit `pos` of w is set, else pool_a.
-__device__ __forceinline__ uint32_t pick_pool(uint32_t w, int pos, uint32_t pool_a, uint32_t pool_b) {
-    const uint32_t mask = uint32_t(int32_t(w << (31 - pos)) >> 31);
-    return (mask & (pool_a ^ pool_b)) ^ pool_a;
-}
-
 // Plane k, operand dword: bytes k of u[0..3], each minus 128.
 __device__ __forceinline__ void byte_planes(const uint32_t *u, uint32_t &p0, uint32_t &p1, uint32_t &p2) {
     const uint32_t a01 = perm(u[1], u[0], 0x05010400u), a23 = perm(u[3], u[2], 0x05010400u);
@@ -193,6 +187,7 @@ struct Gemv2Smem {
     static constexpr bool IQ1 = MEMBER == IQ1_S_R4;
     uint8_t dig[3 * kPlaneStride<N> + (kMaskedA<MEMBER> ? 0 : Gemv2Shape<MEMBER, N>::WK)] __attribute__((aligned(16)));
     float sbs[N / 32] __attribute__((aligned(16)));
+    float nsbs[MEMBER == IQ2_KS ? N / 32 : 4] __attribute__((aligned(16)));  // -16 x 2^-E (IQ2_KS)
     float part[Gemv2Shape<MEMBER, N>::KS][4][kGroupRows];
     int fsum[IQ1 ? N / 32 : 4] __attribute__((aligned(16)));
     uint2_t b8[IQ1 ? IQK_IQ1S_GRID_SIZE : 1];
@@ -216,11 +211,11 @@ constexpr int kExpBlock = MEMBER == IQ2_K ? 64 : 32;
 //     order 0,4,1,5,2,6,3,7 of the grid expansion, so the thread takes
 //     elements 8hp..8hp+7, the pairs 4hp..4hp+3 it holds.
 // One exponent E covers BLOCK (32 or 64) consecutive elements, 2^-E lands in
-// sbs[element / BLOCK].  With `fsum` / `fword`, each 32-element block's /
+// sbs[element / BLOCK] (and -16 x 2^-E in nsbs, when given).  With `fsum` / `fword`, each 32-element block's /
 // 16-element word's sum(f) lands there too; with ZERO_SPAN, the WK bytes
 // after the planes are cleared.
 template <int N, bool TRANSPOSED, bool ZERO_SPAN, int BLOCK, int WK>
-__device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, int *fsum, float *fword, int tid,
+__device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, float *nsbs, int *fsum, float *fword, int tid,
                                                   uint4_t xv) {
     static_assert(BLOCK == 32 || BLOCK == 64, "4 or 8 threads per exponent block");
     const uint32_t wd = uint32_t(tid) >> 1, hp = uint32_t(tid) & 1u;
@@ -290,8 +285,11 @@ __device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, int 
     *reinterpret_cast<uint2_t *>(dig + 0 * kPlaneStride<N> + off) = uint2_t{l0, h0};
     *reinterpret_cast<uint2_t *>(dig + 1 * kPlaneStride<N> + off) = uint2_t{l1, h1};
     *reinterpret_cast<uint2_t *>(dig + 2 * kPlaneStride<N> + off) = uint2_t{l2, h2};
-    if ((tid & (BLOCK / 8 - 1)) == 0)
+    if ((tid & (BLOCK / 8 - 1)) == 0) {
         sbs[tid / (BLOCK / 8)] = finite ? __uint_as_float(uint32_t(127 - E) << 23) : __builtin_nanf("");
+        if (nsbs) nsbs[tid / (BLOCK / 8)] = finite ? __uint_as_float(0x80000000u | (uint32_t(131 - E) << 23))
+                                                   : __builtin_nanf("");
+    }
 }
 
 // -- per-member lane state: loads, floor hash, and the decode ---------------------
@@ -318,25 +316,43 @@ struct LaneIq2ks {
         return h;
     }
 
-    // sub-blocks 8s+2g+h (32 weights, words 2h, 2h+1 of q[s])
-    __device__ __forceinline__ float decode(const uint8_t *abase, bool data, const float *sbs, int g) const {
+    // sub-blocks 8s+2g+h (32 weights, words 2h, 2h+1 of q[s]); sbs / nsbs:
+    // 2^-E and -16 x 2^-E of each 32-element block
+    __device__ __forceinline__ float decode(const uint8_t *abase, bool data, const float *sbs, const float *nsbs,
+                                            int g) const {
         const uint32_t hbg = hb >> (2 * g), abg = ab >> (2 * g);
-        const uint32_t scg[4] = {sc.x >> (8 * g), sc.y >> (8 * g), sc.z >> (8 * g), sc.w >> (8 * g)};
         float acc = 0.f;
         // Scale index x 2^-E and alphabet pool of sub-blocks 8s+2g+h, formed
         // from the scale bytes alone (left to the scheduler: pinning them
         // here measured slower), so the code words meet only their expansion,
-        // the MFMAs and the folds.
+        // the MFMAs and the folds.  The 5-bit indices of super-blocks 2p and
+        // 2p+1 are packed one a byte, byte 2h + (s - 2p): a v_perm takes
+        // byte g of both scale words as (s0, s1, s0, s1), masks keep the
+        // nibble h of each, two masked shifts add the high bits; then each
+        // factor is (idx - 16) 2^-E = fma(float(byte), 2^-E, -16 x 2^-E),
+        // exact as before.  The pool is a bit-select on the alphabet bit.
+        const uint32_t g2 = uint32_t(g) | (uint32_t(g) << 8);
+        const uint32_t selg = (g2 | (g2 << 16)) + 0x04000400u;  // bytes g, 4+g, g, 4+g
         float fac[4][2];
         uint32_t pool[4][2];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const float2 up = *reinterpret_cast<const float2 *>(sbs + 8 * s + 2 * g);
+        for (int sp = 0; sp < 2; ++sp) {
+            const uint32_t pb = perm(sc[2 * sp + 1], sc[2 * sp], selg);
+            const uint32_t u = hbg >> (16 * sp);  // high bits: super-block 2sp at bits h, 2sp+1 at bits 8+h
+            const uint32_t idx4 = (pb & 0x00000F0Fu) | ((pb >> 4) & 0x0F0F0000u) | ((u & 0x101u) << 4) |
+                                  ((u & 0x202u) << 19);
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int idx = int(((scg[s] >> (4 * h)) & 15u) | (((hbg >> (8 * s + h)) & 1u) << 4)) - 16;
-                fac[s][h] = float(idx) * (h ? up.y : up.x);
-                pool[s][h] = pick_pool(abg, 8 * s + h, kV8Base, kV8Shift);
+            for (int t = 0; t < 2; ++t) {
+                const int s = 2 * sp + t;
+                const float2 up = *reinterpret_cast<const float2 *>(sbs + 8 * s + 2 * g);
+                const float2 nup = *reinterpret_cast<const float2 *>(nsbs + 8 * s + 2 * g);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float idx5 = float((idx4 >> (8 * (2 * h + t))) & 0xffu);
+                    fac[s][h] = fmaf(idx5, h ? up.y : up.x, h ? nup.y : nup.x);
+                    const uint32_t m = uint32_t(int32_t(abg << (31 - (8 * s + h))) >> 31);
+                    pool[s][h] = (m & kV8Shift) | (~m & kV8Base);
+                }
             }
         }
         int4_t Dp[2], A[4] = {};
@@ -651,7 +667,8 @@ void gemv_mfma_kernel(Gemv2Args a) {
             }
             if (stager)
                 stage_activations<N, !IQ1, !kMaskedA<MEMBER>, kExpBlock<MEMBER>, S::WK>(
-                    sm.dig, sm.sbs, IQ1 ? sm.fsum : nullptr, MEMBER == IQ2_K ? sm.fw : nullptr, tid, xv);
+                    sm.dig, sm.sbs, MEMBER == IQ2_KS ? sm.nsbs : nullptr, IQ1 ? sm.fsum : nullptr,
+                    MEMBER == IQ2_K ? sm.fw : nullptr, tid, xv);
             __syncthreads();
             const int ai = l & 15;  // this lane's A row
             const bool data = (ai >> 2) == g && (ai & 3) < 3;
@@ -663,7 +680,7 @@ void gemv_mfma_kernel(Gemv2Args a) {
             if constexpr (IQ1)
                 acc = lane.decode(abase, data, sbs, sm.fsum + (S::WK / 32) * kq, sm.b8, g);
             else if constexpr (MEMBER == IQ2_KS)
-                acc = lane.decode(abase, data, sbs, g);
+                acc = lane.decode(abase, data, sbs, sm.nsbs + (S::WK / 32) * kq, g);
             else
                 acc = lane.decode(abase, sm.sbs + (S::WK / 64) * kq, sm.fw + (S::WK / 16) * kq, sm.ktab, g);
         }
