@@ -134,6 +134,20 @@ __device__ __forceinline__ uint32_t half_row_mirror(uint32_t v) {
 
 __device__ __forceinline__ int digits_sum(int4_t d) { return (((d.z << 8) + d.y) << 8) + d.x; }
 
+// 8 x the low / high 16 bits of v: one SDWA shift each.
+__device__ __forceinline__ uint32_t lo16_x8(uint32_t v) {
+    uint32_t r;
+    asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_0"
+        : "=v"(r) : "v"(v));
+    return r;
+}
+__device__ __forceinline__ uint32_t hi16_x8(uint32_t v) {
+    uint32_t r;
+    asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_1"
+        : "=v"(r) : "v"(v));
+    return r;
+}
+
 // Keeps a value computed where it stands.  The masked A reads split a decode
 // into one block per super-block, and without a use in its own block each
 // fold would be sunk behind the last stream word, into every wavefront's tail.
@@ -211,8 +225,9 @@ constexpr int kExpBlock = MEMBER == IQ2_K ? 64 : 32;
 //     order 0,4,1,5,2,6,3,7 of the grid expansion, so the thread takes
 //     elements 8hp..8hp+7, the pairs 4hp..4hp+3 it holds.
 // One exponent E covers BLOCK (32 or 64) consecutive elements, 2^-E lands in
-// sbs[element / BLOCK] (and -16 x 2^-E in nsbs, when given).  With `fsum` / `fword`, each 32-element block's /
-// 16-element word's sum(f) lands there too; with ZERO_SPAN, the WK bytes
+// sbs[element / BLOCK] (and -16 x 2^-E in nsbs, when given).  With `fsum`,
+// each 32-element block's 2 sum(f) lands there too, with `fword` each
+// 16-element word's sum(f); with ZERO_SPAN, the WK bytes
 // after the planes are cleared.
 template <int N, bool TRANSPOSED, bool ZERO_SPAN, int BLOCK, int WK>
 __device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, float *nsbs, int *fsum, float *fword, int tid,
@@ -276,7 +291,7 @@ __device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, floa
         f += quad_xor<1>(f);  // the 16-element word
         if (fword && (tid & 1) == 0) fword[tid >> 1] = float(int(f));
         f += quad_xor<2>(f);  // the 32-element block
-        if (fsum && (tid & 3) == 0) fsum[tid >> 2] = int(f);
+        if (fsum && (tid & 3) == 0) fsum[tid >> 2] = 2 * int(f);
     }
     uint32_t l0, l1, l2, h0, h1, h2;
     byte_planes(u0, l0, l1, l2);
@@ -516,22 +531,25 @@ struct LaneIq1s {
 
     // blocks 16i+4g+b (32 weights: index bytes of dword b of qv[i], qh word b
     // of qh[i]).  The table holds 8g + 1; a block with a negative shift uses
-    // 8g - 1, which takes 2 sum(f) off its digit sum.
-    __device__ __forceinline__ float decode(const uint8_t *abase, bool data, const float *sbs, const int *fsum,
+    // 8g - 1, which takes 2 sum(f) off its digit sum.  fsum2: 2 sum(f) of
+    // each 32-element block.
+    __device__ __forceinline__ float decode(const uint8_t *abase, bool data, const float *sbs, const int *fsum2,
                                             const uint2_t *b8, int g) const {
         // Before any index byte is needed: each block's scale x 2^-E and its
-        // negative-shift correction 2 sum(f) (or 0).
+        // negative-shift correction 2 sum(f) (or 0).  2s + 1 of the two
+        // blocks of a qh dword lands in its bytes 0 and 2 in two ops.
         float acc = 0.f, fac[4 * NI];
         int corr[4 * NI];
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const float4 upv = *reinterpret_cast<const float4 *>(sbs + 16 * i + 4 * g);
-            const int4_t fsv = *reinterpret_cast<const int4_t *>(fsum + 16 * i + 4 * g);
+            const int4_t fsv = *reinterpret_cast<const int4_t *>(fsum2 + 16 * i + 4 * g);
+            const uint32_t odd[2] = {((qh[i].x >> 11) & 0x000E000Eu) | 0x00010001u,
+                                     ((qh[i].y >> 11) & 0x000E000Eu) | 0x00010001u};
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-                const uint32_t hw = (qh[i][b >> 1] >> (16 * (b & 1))) & 0xffffu;
-                fac[4 * i + b] = float(2 * ((hw >> 12) & 7u) + 1) * upv[b];
-                corr[4 * i + b] = (2 * fsv[b]) & -int(hw >> 15);
+                fac[4 * i + b] = float((odd[b >> 1] >> (16 * (b & 1))) & 0xffu) * upv[b];
+                corr[4 * i + b] = fsv[b] & (int32_t(qh[i][b >> 1] << (16 - 16 * (b & 1))) >> 31);
                 pin(fac[4 * i + b]);
                 pin(corr[4 * i + b]);
             }
@@ -544,12 +562,21 @@ struct LaneIq1s {
                 const int i = c >> 2, b = c & 3;
                 if ((b & 1) == 0) read_a(A, abase + 512 * i + 32 * b, data);  // blocks b, b+1
                 const uint32_t qw = qv[i][b];
-                const uint32_t hw = (qh[i][b >> 1] >> (16 * (b & 1))) & 0xffffu;
+                const uint32_t hw = (qh[i][b >> 1] >> (16 * (b & 1))) & 0xfffu;  // the four 3-bit high fields
+                // Grid indices of groups 2t, 2t+1 as the 16-bit halves of
+                // ix[t]: low bytes 2t, 2t+1 of qw placed by a v_perm, high
+                // fields 2t, 2t+1 of hw by one multiply that copies hw to
+                // two places (bits 8 and 21 up; for t = 1, 2 and 15 up): the
+                // copies do not overlap, so no carries, and the mask keeps
+                // exactly the wanted fields at bits 8-10 and 24-26.
+                const uint32_t ix[2] = {
+                    (__umul24(hw, 0x200100u) & 0x07000700u) | perm(qw, qw, 0x0c010c00u),
+                    (__umul24(hw, 0x008004u) & 0x07000700u) | perm(qw, qw, 0x0c030c02u)};
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {  // 8-weight groups 2t, 2t+1 of the block
-                    const uint32_t i0 = ((qw >> (16 * t)) & 0xffu) | (((hw >> (6 * t)) & 7u) << 8);
-                    const uint32_t i1 = ((qw >> (16 * t + 8)) & 0xffu) | (((hw >> (6 * t + 3)) & 7u) << 8);
-                    const uint2_t w0 = b8[i0], w1 = b8[i1];
+                    const uint8_t *b8b = reinterpret_cast<const uint8_t *>(b8);
+                    const uint2_t w0 = *reinterpret_cast<const uint2_t *>(b8b + lo16_x8(ix[t]));
+                    const uint2_t w1 = *reinterpret_cast<const uint2_t *>(b8b + hi16_x8(ix[t]));
                     D = mfma(A[2 * (b & 1) + t], int4_t{int(w0.x), int(w0.y), int(w1.x), int(w1.y)},
                              t ? D : int4_t{0, 0, 0, 0});
                 }
