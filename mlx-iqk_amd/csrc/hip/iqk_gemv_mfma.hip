@@ -188,21 +188,24 @@ __device__ __forceinline__ int4_t read_a_all(const uint8_t *p) {
 }
 
 // Whether a member's kernel reads A only in the data lanes (fewer LDS bytes,
-// more live registers) or in every lane from a zero span.  IQ2_K, with a fold
-// per 16 weights, is register-bound and reads in every lane.
-template <int MEMBER>
-constexpr bool kMaskedA = MEMBER != IQ2_K;
+// more live registers: the other lanes hold zeros for the whole kernel) or in
+// every lane, the others from a zero span.  IQ2_K, with a fold per 16
+// weights, is register-bound and reads in every lane, and so does every
+// member at two row blocks per wavefront, where each read serves both.
+template <int MEMBER, int R>
+constexpr bool kMaskedA = MEMBER != IQ2_K && R == 1;
 
 // Shared memory of one workgroup: the activations' three byte planes (and a
-// zero span when every lane reads A), 2^-E per 32-element block, the wavefronts' partial row sums,
-// and for IQ1_S_R4 the expanded grid and each block's integer sum(f).
-template <int MEMBER, int N>
+// zero span when every lane reads A), 2^-E per 32-element block, the
+// wavefronts' partial row sums (32 R rows), and for IQ1_S_R4 the expanded
+// grid and each block's integer 2 sum(f).
+template <int MEMBER, int N, int R>
 struct Gemv2Smem {
     static constexpr bool IQ1 = MEMBER == IQ1_S_R4;
-    uint8_t dig[3 * kPlaneStride<N> + (kMaskedA<MEMBER> ? 0 : Gemv2Shape<MEMBER, N>::WK)] __attribute__((aligned(16)));
+    uint8_t dig[3 * kPlaneStride<N> + (kMaskedA<MEMBER, R> ? 0 : Gemv2Shape<MEMBER, N>::WK)] __attribute__((aligned(16)));
     float sbs[N / 32] __attribute__((aligned(16)));
     float nsbs[MEMBER == IQ2_KS ? N / 32 : 4] __attribute__((aligned(16)));  // -16 x 2^-E (IQ2_KS)
-    float part[Gemv2Shape<MEMBER, N>::KS][4][kGroupRows];
+    float part[Gemv2Shape<MEMBER, N>::KS][4][kGroupRows * R];
     int fsum[IQ1 ? N / 32 : 4] __attribute__((aligned(16)));
     uint2_t b8[IQ1 ? IQK_IQ1S_GRID_SIZE : 1];
     uint2_t ktab[MEMBER == IQ2_K ? 32 : 1];
@@ -331,12 +334,12 @@ struct LaneIq2ks {
         return h;
     }
 
-    // sub-blocks 8s+2g+h (32 weights, words 2h, 2h+1 of q[s]); sbs / nsbs:
-    // 2^-E and -16 x 2^-E of each 32-element block
-    __device__ __forceinline__ float decode(const uint8_t *abase, bool data, const float *sbs, const float *nsbs,
-                                            int g) const {
-        const uint32_t hbg = hb >> (2 * g), abg = ab >> (2 * g);
-        float acc = 0.f;
+    // Sub-blocks 8s+2g+h (32 weights, words 2h, 2h+1 of q[s]) of R rows, one
+    // lane instance each, which share every A read; sbs / nsbs: 2^-E and
+    // -16 x 2^-E of each 32-element block.
+    template <int R>
+    __device__ __forceinline__ static void decode(const LaneIq2ks (&ln)[R], const uint8_t *abase, bool data,
+                                                  const float *sbs, const float *nsbs, int g, float (&out)[R]) {
         // Scale index x 2^-E and alphabet pool of sub-blocks 8s+2g+h, formed
         // from the scale bytes alone (left to the scheduler: pinning them
         // here measured slower), so the code words meet only their expansion,
@@ -348,49 +351,71 @@ struct LaneIq2ks {
         // exact as before.  The pool is a bit-select on the alphabet bit.
         const uint32_t g2 = uint32_t(g) | (uint32_t(g) << 8);
         const uint32_t selg = (g2 | (g2 << 16)) + 0x04000400u;  // bytes g, 4+g, g, 4+g
-        float fac[4][2];
-        uint32_t pool[4][2];
+        float fac[R][4][2];
+        uint32_t pool[R][4][2], idx4[R];
+        // Super-block s's factors and pools.  One row block forms them all
+        // before the first code word; two form each just before its MFMAs
+        // (the registers of all four would cost a wavefront per SIMD).
+        const auto prep = [&](int s) {
+            const int sp = s >> 1, t = s & 1;
 #pragma unroll
-        for (int sp = 0; sp < 2; ++sp) {
-            const uint32_t pb = perm(sc[2 * sp + 1], sc[2 * sp], selg);
-            const uint32_t u = hbg >> (16 * sp);  // high bits: super-block 2sp at bits h, 2sp+1 at bits 8+h
-            const uint32_t idx4 = (pb & 0x00000F0Fu) | ((pb >> 4) & 0x0F0F0000u) | ((u & 0x101u) << 4) |
-                                  ((u & 0x202u) << 19);
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const int s = 2 * sp + t;
+            for (int r = 0; r < R; ++r) {
+                const uint32_t hbg = ln[r].hb >> (2 * g), abg = ln[r].ab >> (2 * g);
+                if (t == 0) {
+                    const uint32_t pb = perm(ln[r].sc[2 * sp + 1], ln[r].sc[2 * sp], selg);
+                    const uint32_t u = hbg >> (16 * sp);  // high bits: super-block 2sp at bits h, 2sp+1 at 8+h
+                    idx4[r] = (pb & 0x00000F0Fu) | ((pb >> 4) & 0x0F0F0000u) | ((u & 0x101u) << 4) |
+                              ((u & 0x202u) << 19);
+                }
                 const float2 up = *reinterpret_cast<const float2 *>(sbs + 8 * s + 2 * g);
                 const float2 nup = *reinterpret_cast<const float2 *>(nsbs + 8 * s + 2 * g);
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    const float idx5 = float((idx4 >> (8 * (2 * h + t))) & 0xffu);
-                    fac[s][h] = fmaf(idx5, h ? up.y : up.x, h ? nup.y : nup.x);
+                    const float idx5 = float((idx4[r] >> (8 * (2 * h + t))) & 0xffu);
+                    fac[r][s][h] = fmaf(idx5, h ? up.y : up.x, h ? nup.y : nup.x);
                     const uint32_t m = uint32_t(int32_t(abg << (31 - (8 * s + h))) >> 31);
-                    pool[s][h] = (m & kV8Shift) | (~m & kV8Base);
+                    pool[r][s][h] = (m & kV8Shift) | (~m & kV8Base);
                 }
             }
+        };
+        if constexpr (R == 1) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) prep(s);
         }
-        int4_t Dp[2], A[4] = {};
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.f;
+        int4_t Dp[R][2], A[4] = {};
 #pragma unroll
         for (int s = 0; s <= 4; ++s) {
-            int4_t D[2];
+            int4_t D[R][2];
             if (s < 4) {
+                if constexpr (R > 1) prep(s);
                 read_a(A, abase + 256 * s, data);
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    D[h] = mfma(A[2 * h], codes_to_i8(q[s][2 * h], pool[s][h]), int4_t{0, 0, 0, 0});
-                    D[h] = mfma(A[2 * h + 1], codes_to_i8(q[s][2 * h + 1], pool[s][h]), D[h]);
-                }
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        D[r][h] = mfma(A[2 * h], codes_to_i8(ln[r].q[s][2 * h], pool[r][s][h]), int4_t{0, 0, 0, 0});
+                        D[r][h] = mfma(A[2 * h + 1], codes_to_i8(ln[r].q[s][2 * h + 1], pool[r][s][h]), D[r][h]);
+                    }
             }
             if (s > 0) {  // fold the previous super-block while this one's MFMAs run
                 const int sp = s - 1;
 #pragma unroll
-                for (int h = 0; h < 2; ++h) acc = fmaf(float(digits_sum(Dp[h])), fac[sp][h], acc);
-                pin(acc);
+                for (int r = 0; r < R; ++r) {
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) acc[r] = fmaf(float(digits_sum(Dp[r][h])), fac[r][sp][h], acc[r]);
+                    pin(acc[r]);
+                }
             }
-            if (s < 4) { Dp[0] = D[0]; Dp[1] = D[1]; }
+            if (s < 4) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) { Dp[r][0] = D[r][0]; Dp[r][1] = D[r][1]; }
+            }
         }
-        return acc * half_bits_to_float(dvb);
+#pragma unroll
+        for (int r = 0; r < R; ++r) out[r] = acc[r] * half_bits_to_float(ln[r].dvb);
     }
 };
 
@@ -425,60 +450,93 @@ struct LaneIq2k {
     // of a super-block, which share one activation exponent.  The constant
     // part idx * off * sum(f) takes one fma per word from the word's integer
     // activation sum fw.  A lane folds once per super-block.
-    __device__ __forceinline__ float decode(const uint8_t *abase, const float *sbs, const float *fw,
-                                            const uint2_t *ktab, int g) const {
+    // R rows, one lane instance each, share every A read.
+    template <int R>
+    __device__ __forceinline__ static void decode(const LaneIq2k (&ln)[R], const uint8_t *abase, const float *sbs,
+                                                  const float *fw, const uint2_t *ktab, int g, float (&out)[R]) {
         // This lane's scale word of super-block s is u16 g of the pair
         // (sc.y:sc.x) or (sc.w:sc.z); one v_perm spreads its two bytes to
         // (b0, b0, b1, b1), and shifts put nibble j at bits 3-6 of byte j.
         const uint32_t selg = 0x01010000u + uint32_t(2 * g) * 0x01010101u;
-        const uint32_t scp[4] = {perm(sc0.y, sc0.x, selg), perm(sc0.w, sc0.z, selg), perm(sc1.y, sc1.x, selg),
-                                 perm(sc1.w, sc1.z, selg)};
         // alphabet bits of super-block s: byte 2s + g/2 of ex, bits 4(g%2) + j
         const int exs = 8 * (g >> 1) + 4 * (g & 1);
-        const uint32_t exg[2] = {ex.x >> exs, ex.y >> exs};
         // Before any code word is needed: each super-block's d x 2^-E, its
         // constant part sum_j (idx off)_j fw_j, and its four word pools.
-        float acc = 0.f, dfac[4], offs[4];
-        uint32_t pools[4][4];
+        float dfac[R][4], offs[R][4];
+        uint32_t pools[R][4][4], scp[R][4], exg[R][2];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const float4 fwv = *reinterpret_cast<const float4 *>(fw + 16 * s + 4 * g);
-            dfac[s] = half_bits_to_float((dv[s >> 1] >> (16 * (s & 1))) & 0xffffu) * sbs[4 * s + g];
-            offs[s] = 0.f;
-            // byte j: the table's byte offset 8 (alpha_j << 4 | nib_j) of word
-            // j; the multiply copies alphabet bit j to bit 8j (no two copies
-            // meet, so no carries; pinned, or it becomes a quarter-rate
-            // 32-bit multiply by the shifted constant)
-            uint32_t a8 = __umul24((exg[s >> 1] >> (16 * (s & 1))) & 15u, 0x204081u);
-            pin(a8);
-            const uint32_t kofs = ((scp[s] << 3) & 0x00780078u) | ((scp[s] >> 1) & 0x78007800u) |
-                                  ((a8 & 0x01010101u) << 7);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint2_t e = *reinterpret_cast<const uint2_t *>(reinterpret_cast<const uint8_t *>(ktab) +
-                                                                     ((kofs >> (8 * j)) & 0xffu));
-                pools[s][j] = e.x;
-                offs[s] = fmaf(__uint_as_float(e.y), fwv[j], offs[s]);
-            }
+        for (int r = 0; r < R; ++r) {
+            scp[r][0] = perm(ln[r].sc0.y, ln[r].sc0.x, selg);
+            scp[r][1] = perm(ln[r].sc0.w, ln[r].sc0.z, selg);
+            scp[r][2] = perm(ln[r].sc1.y, ln[r].sc1.x, selg);
+            scp[r][3] = perm(ln[r].sc1.w, ln[r].sc1.z, selg);
+            exg[r][0] = ln[r].ex.x >> exs;
+            exg[r][1] = ln[r].ex.y >> exs;
         }
-        int4_t Wp;
+        // Super-block s's factors and pools.  One row block forms them all
+        // before the first code word; two form each just before its MFMAs
+        // (the registers of all four would cost a wavefront per SIMD).
+        const auto prep = [&](int s) {
+            const float4 fwv = *reinterpret_cast<const float4 *>(fw + 16 * s + 4 * g);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                dfac[r][s] = half_bits_to_float((ln[r].dv[s >> 1] >> (16 * (s & 1))) & 0xffffu) * sbs[4 * s + g];
+                offs[r][s] = 0.f;
+                // byte j: the table's byte offset 8 (alpha_j << 4 | nib_j) of
+                // word j; the multiply copies alphabet bit j to bit 8j (no two
+                // copies meet, so no carries; pinned, or it becomes a
+                // quarter-rate 32-bit multiply by the shifted constant)
+                uint32_t a8 = __umul24((exg[r][s >> 1] >> (16 * (s & 1))) & 15u, 0x204081u);
+                pin(a8);
+                const uint32_t kofs = ((scp[r][s] << 3) & 0x00780078u) | ((scp[r][s] >> 1) & 0x78007800u) |
+                                      ((a8 & 0x01010101u) << 7);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint2_t e = *reinterpret_cast<const uint2_t *>(reinterpret_cast<const uint8_t *>(ktab) +
+                                                                         ((kofs >> (8 * j)) & 0xffu));
+                    pools[r][s][j] = e.x;
+                    offs[r][s] = fmaf(__uint_as_float(e.y), fwv[j], offs[r][s]);
+                }
+            }
+        };
+        if constexpr (R == 1) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) prep(s);
+        }
+        float acc[R];
+        int4_t Wp[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.f;
 #pragma unroll
         for (int s = 0; s <= 4; ++s) {
-            int4_t W = {0, 0, 0, 0};
-            if (s < 4) {
+            int4_t W[R];
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    W = mfma(read_a_all(abase + 256 * s + 16 * j), codes_to_i8(q[s][j], pools[s][j]), W);
+            for (int r = 0; r < R; ++r) W[r] = int4_t{0, 0, 0, 0};
+            if (s < 4) {
+                if constexpr (R > 1) prep(s);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int4_t a = read_a_all(abase + 256 * s + 16 * j);
+#pragma unroll
+                    for (int r = 0; r < R; ++r) W[r] = mfma(a, codes_to_i8(ln[r].q[s][j], pools[r][s][j]), W[r]);
+                }
             }
             if (s > 0) {  // fold the previous super-block while this one's MFMAs run
                 const int sp = s - 1;
-                const float sum = fmaf(float(Wp.z), 65536.f, fmaf(float(Wp.y), 256.f, float(Wp.x)));
-                acc = fmaf(fmaf(2.f, sum, offs[sp]), dfac[sp], acc);
-                pin(acc);
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const float sum = fmaf(float(Wp[r].z), 65536.f, fmaf(float(Wp[r].y), 256.f, float(Wp[r].x)));
+                    acc[r] = fmaf(fmaf(2.f, sum, offs[r][sp]), dfac[r][sp], acc[r]);
+                    pin(acc[r]);
+                }
             }
-            if (s < 4) Wp = W;
+            if (s < 4) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) Wp[r] = W[r];
+            }
         }
-        return acc;
+#pragma unroll
+        for (int r = 0; r < R; ++r) out[r] = acc[r];
     }
 };
 
@@ -533,61 +591,92 @@ struct LaneIq1s {
     // of qh[i]).  The table holds 8g + 1; a block with a negative shift uses
     // 8g - 1, which takes 2 sum(f) off its digit sum.  fsum2: 2 sum(f) of
     // each 32-element block.
-    __device__ __forceinline__ float decode(const uint8_t *abase, bool data, const float *sbs, const int *fsum2,
-                                            const uint2_t *b8, int g) const {
-        // Before any index byte is needed: each block's scale x 2^-E and its
-        // negative-shift correction 2 sum(f) (or 0).  2s + 1 of the two
-        // blocks of a qh dword lands in its bytes 0 and 2 in two ops.
-        float acc = 0.f, fac[4 * NI];
-        int corr[4 * NI];
+    // R rows, one lane instance each, share every A read.
+    template <int R>
+    __device__ __forceinline__ static void decode(const LaneIq1s (&ln)[R], const uint8_t *abase, bool data,
+                                                  const float *sbs, const int *fsum2, const uint2_t *b8, int g,
+                                                  float (&out)[R]) {
+        // Each block's scale x 2^-E and its negative-shift correction
+        // 2 sum(f) (or 0); 2s + 1 of the two blocks of a qh dword lands in
+        // its bytes 0 and 2 in two ops.  One row block forms them all before
+        // the first index byte; two form each pair of blocks just before its
+        // MFMAs (the registers of all would cost a wavefront per SIMD).
+        float fac[R][4 * NI];
+        int corr[R][4 * NI];
+        const auto prep = [&](int i, int bp) {  // blocks 4i + 2bp, +1
+            const float2 upv = *reinterpret_cast<const float2 *>(sbs + 16 * i + 4 * g + 2 * bp);
+            const int2 fsv = *reinterpret_cast<const int2 *>(fsum2 + 16 * i + 4 * g + 2 * bp);
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const float4 upv = *reinterpret_cast<const float4 *>(sbs + 16 * i + 4 * g);
-            const int4_t fsv = *reinterpret_cast<const int4_t *>(fsum2 + 16 * i + 4 * g);
-            const uint32_t odd[2] = {((qh[i].x >> 11) & 0x000E000Eu) | 0x00010001u,
-                                     ((qh[i].y >> 11) & 0x000E000Eu) | 0x00010001u};
+            for (int r = 0; r < R; ++r) {
+                const uint32_t qh = ln[r].qh[i][bp];
+                const uint32_t odd = ((qh >> 11) & 0x000E000Eu) | 0x00010001u;
 #pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                fac[4 * i + b] = float((odd[b >> 1] >> (16 * (b & 1))) & 0xffu) * upv[b];
-                corr[4 * i + b] = fsv[b] & (int32_t(qh[i][b >> 1] << (16 - 16 * (b & 1))) >> 31);
-                pin(fac[4 * i + b]);
-                pin(corr[4 * i + b]);
+                for (int h = 0; h < 2; ++h) {
+                    const int c = 4 * i + 2 * bp + h;
+                    fac[r][c] = float((odd >> (16 * h)) & 0xffu) * (h ? upv.y : upv.x);
+                    corr[r][c] = (h ? fsv.y : fsv.x) & (int32_t(qh << (16 - 16 * h)) >> 31);
+                    pin(fac[r][c]);
+                    pin(corr[r][c]);
+                }
+            }
+        };
+        if constexpr (R == 1) {
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                prep(i, 0);
+                prep(i, 1);
             }
         }
-        int4_t Dp, A[4] = {};
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.f;
+        const uint8_t *b8b = reinterpret_cast<const uint8_t *>(b8);
+        int4_t Dp[R], A[4] = {};
 #pragma unroll
         for (int c = 0; c <= 4 * NI; ++c) {  // block c = 4i + b
-            int4_t D;
+            int4_t D[R];
             if (c < 4 * NI) {
                 const int i = c >> 2, b = c & 3;
-                if ((b & 1) == 0) read_a(A, abase + 512 * i + 32 * b, data);  // blocks b, b+1
-                const uint32_t qw = qv[i][b];
-                const uint32_t hw = (qh[i][b >> 1] >> (16 * (b & 1))) & 0xfffu;  // the four 3-bit high fields
-                // Grid indices of groups 2t, 2t+1 as the 16-bit halves of
-                // ix[t]: low bytes 2t, 2t+1 of qw placed by a v_perm, high
-                // fields 2t, 2t+1 of hw by one multiply that copies hw to
-                // two places (bits 8 and 21 up; for t = 1, 2 and 15 up): the
-                // copies do not overlap, so no carries, and the mask keeps
-                // exactly the wanted fields at bits 8-10 and 24-26.
-                const uint32_t ix[2] = {
-                    (__umul24(hw, 0x200100u) & 0x07000700u) | perm(qw, qw, 0x0c010c00u),
-                    (__umul24(hw, 0x008004u) & 0x07000700u) | perm(qw, qw, 0x0c030c02u)};
+                if ((b & 1) == 0) {  // blocks b, b+1
+                    if constexpr (R > 1) prep(i, b >> 1);
+                    read_a(A, abase + 512 * i + 32 * b, data);
+                }
 #pragma unroll
-                for (int t = 0; t < 2; ++t) {  // 8-weight groups 2t, 2t+1 of the block
-                    const uint8_t *b8b = reinterpret_cast<const uint8_t *>(b8);
-                    const uint2_t w0 = *reinterpret_cast<const uint2_t *>(b8b + lo16_x8(ix[t]));
-                    const uint2_t w1 = *reinterpret_cast<const uint2_t *>(b8b + hi16_x8(ix[t]));
-                    D = mfma(A[2 * (b & 1) + t], int4_t{int(w0.x), int(w0.y), int(w1.x), int(w1.y)},
-                             t ? D : int4_t{0, 0, 0, 0});
+                for (int r = 0; r < R; ++r) {
+                    const uint32_t qw = ln[r].qv[i][b];
+                    const uint32_t hw = (ln[r].qh[i][b >> 1] >> (16 * (b & 1))) & 0xfffu;  // four 3-bit high fields
+                    // Grid indices of groups 2t, 2t+1 as the 16-bit halves of
+                    // ix[t]: low bytes 2t, 2t+1 of qw placed by a v_perm, high
+                    // fields 2t, 2t+1 of hw by one multiply that copies hw to
+                    // two places (bits 8 and 21 up; for t = 1, 2 and 15 up):
+                    // the copies do not overlap, so no carries, and the mask
+                    // keeps exactly the wanted fields at bits 8-10 and 24-26.
+                    const uint32_t ix[2] = {
+                        (__umul24(hw, 0x200100u) & 0x07000700u) | perm(qw, qw, 0x0c010c00u),
+                        (__umul24(hw, 0x008004u) & 0x07000700u) | perm(qw, qw, 0x0c030c02u)};
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {  // 8-weight groups 2t, 2t+1 of the block
+                        const uint2_t w0 = *reinterpret_cast<const uint2_t *>(b8b + lo16_x8(ix[t]));
+                        const uint2_t w1 = *reinterpret_cast<const uint2_t *>(b8b + hi16_x8(ix[t]));
+                        D[r] = mfma(A[2 * (b & 1) + t], int4_t{int(w0.x), int(w0.y), int(w1.x), int(w1.y)},
+                                    t ? D[r] : int4_t{0, 0, 0, 0});
+                    }
                 }
             }
             if (c > 0) {
-                acc = fmaf(float(digits_sum(Dp) - corr[c - 1]), fac[c - 1], acc);
-                pin(acc);
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    acc[r] = fmaf(float(digits_sum(Dp[r]) - corr[r][c - 1]), fac[r][c - 1], acc[r]);
+                    pin(acc[r]);
+                }
             }
-            if (c < 4 * NI) Dp = D;
+            if (c < 4 * NI) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) Dp[r] = D[r];
+            }
         }
-        return acc * (0.125f * half_bits_to_float(dvb));
+#pragma unroll
+        for (int r = 0; r < R; ++r) out[r] = acc[r] * (0.125f * half_bits_to_float(ln[r].dvb));
     }
 };
 
@@ -604,24 +693,29 @@ enum GemvMode : int {
                   // expert's rows once: the run's first pair does the run
 };
 
-// Six wavefronts per SIMD: three workgroups of eight (N = 4096) or six of
-// four (N = 2048) per CU, so a 1-token routed decode's 768 workgroups are
-// resident at once.  kUnion keeps each lane's expanded weights in registers
-// across its run (134-182 VGPRs): two or three wavefronts per SIMD, no spills.
-template <int MEMBER, int N, bool FLOOR, int MODE>
+// R = 1: six wavefronts per SIMD, three workgroups of eight (N = 4096) or
+// six of four (N = 2048) per CU, so a 1-token routed decode's 768
+// workgroups are resident at once.  R = 2 (dispatches of many workgroups):
+// each wavefront takes 32 rows, two MFMA column blocks that share every A
+// read, so a workgroup stages its activations for 64 rows; four wavefronts
+// per SIMD.  kUnion keeps each lane's expanded weights in registers across
+// its run (134-182 VGPRs): two or three wavefronts per SIMD, no spills.
+template <int MEMBER, int N, bool FLOOR, int MODE, int R>
 __global__ __launch_bounds__((Gemv2Shape<MEMBER, N>::THREADS))
-__attribute__((amdgpu_waves_per_eu(MODE == kUnion ? 2 : 6)))
+__attribute__((amdgpu_waves_per_eu(MODE == kUnion ? 2 : R == 2 ? 5 : 6)))
 void gemv_mfma_kernel(Gemv2Args a) {
     using S = Gemv2Shape<MEMBER, N>;
     constexpr int KS = S::KS;
-    __shared__ Gemv2Smem<MEMBER, N> sm;
+    constexpr int ROWS = kGroupRows * R;  // rows per workgroup
+    static_assert(MODE != kUnion || R == 1, "the union form keeps one row block per wavefront");
+    __shared__ Gemv2Smem<MEMBER, N, R> sm;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, l = tid & 63;
     const int n = l & 15, g = l >> 4;
     const int kq = wave % KS, tile = wave / KS;
     const uint32_t m0 = MODE == kPairs ? blockIdx.z * a.pairs_per_row + blockIdx.y : blockIdx.z;
-    const uint32_t rowg = blockIdx.x * kGroupRows;
+    const uint32_t rowg = blockIdx.x * ROWS;
 
     // The run of pairs this workgroup serves: one pair, or for kUnion every
     // pair of a run of equal ids (workgroups of the run's other pairs exit).
@@ -664,9 +758,9 @@ void gemv_mfma_kernel(Gemv2Args a) {
     const uint32_t e_raw = a.sel[m0];
     const bool valid = e_raw < a.num_experts;  // uniform per workgroup
     const uint32_t e = valid ? e_raw : 0u;
-    const uint32_t row = e * a.out_features + rowg + 16 * tile + n;
-    LaneOf<MEMBER, N> lane;
-    lane.load(a, row, kq, g);
+    LaneOf<MEMBER, N> lane[R];  // rows rowg + 16 (R tile + r) + n
+#pragma unroll
+    for (int r = 0; r < R; ++r) lane[r].load(a, e * a.out_features + rowg + 16 * (R * tile + r) + n, kq, g);
 
     // One pair's contraction.  Outside kUnion it runs once, straight-line: a
     // loop here, even of one trip, costs the pair kernels registers.
@@ -677,10 +771,13 @@ void gemv_mfma_kernel(Gemv2Args a) {
             x_ok = tok < a.n_x_rows;
             load_x(x_ok ? tok : 0u, xv);
         }
-        float acc;
+        float acc[R];
         if constexpr (FLOOR) {
-            const uint32_t h = xv.x + 3u * xv.y + 5u * xv.z + 7u * xv.w + lane.hash();
-            acc = float(h & 0xffu);
+            uint32_t h = xv.x + 3u * xv.y + 5u * xv.z + 7u * xv.w;
+#pragma unroll
+            for (int r = 0; r < R; ++r) h += lane[r].hash();
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] = float((h >> r) & 0xffu);
         } else {
             if (q == 0) {
                 if constexpr (GRID) {
@@ -693,30 +790,34 @@ void gemv_mfma_kernel(Gemv2Args a) {
                 if (KTAB && tid < 32) sm.ktab[tid] = ktv;
             }
             if (stager)
-                stage_activations<N, !IQ1, !kMaskedA<MEMBER>, kExpBlock<MEMBER>, S::WK>(
+                stage_activations<N, !IQ1, !kMaskedA<MEMBER, R>, kExpBlock<MEMBER>, S::WK>(
                     sm.dig, sm.sbs, MEMBER == IQ2_KS ? sm.nsbs : nullptr, IQ1 ? sm.fsum : nullptr,
                     MEMBER == IQ2_K ? sm.fw : nullptr, tid, xv);
             __syncthreads();
             const int ai = l & 15;  // this lane's A row
             const bool data = (ai >> 2) == g && (ai & 3) < 3;
+            constexpr bool MASKED = kMaskedA<MEMBER, R>;
             constexpr int LANE_K = IQ1 ? 128 : 64;
-            const uint8_t *abase =
-                sm.dig + (data || kMaskedA<MEMBER> ? (ai & 3) * kPlaneStride<N> + S::WK * kq + LANE_K * g
-                                                   : 3 * kPlaneStride<N>);
+            const uint8_t *abase = sm.dig + (data || MASKED ? (ai & 3) * kPlaneStride<N> + S::WK * kq + LANE_K * g
+                                                            : 3 * kPlaneStride<N>);
+            const bool reads = data || !MASKED;  // lanes that read A
             const float *sbs = sm.sbs + (S::WK / 32) * kq;
+            using Lane = LaneOf<MEMBER, N>;
             if constexpr (IQ1)
-                acc = lane.decode(abase, data, sbs, sm.fsum + (S::WK / 32) * kq, sm.b8, g);
+                Lane::template decode<R>(lane, abase, reads, sbs, sm.fsum + (S::WK / 32) * kq, sm.b8, g, acc);
             else if constexpr (MEMBER == IQ2_KS)
-                acc = lane.decode(abase, data, sbs, sm.nsbs + (S::WK / 32) * kq, g);
+                Lane::template decode<R>(lane, abase, reads, sbs, sm.nsbs + (S::WK / 32) * kq, g, acc);
             else
-                acc = lane.decode(abase, sm.sbs + (S::WK / 64) * kq, sm.fw + (S::WK / 16) * kq, sm.ktab, g);
+                Lane::template decode<R>(lane, abase, sm.sbs + (S::WK / 64) * kq, sm.fw + (S::WK / 16) * kq,
+                                         sm.ktab, g, acc);
         }
         // Partials of the row's lanes and wavefronts: wave 0 sums them after
         // the barrier; the next pair's staging and partials come only after
         // its own barrier, which wave 0 reaches after summing.
-        sm.part[kq][g][16 * tile + n] = acc;
+#pragma unroll
+        for (int r = 0; r < R; ++r) sm.part[kq][g][16 * (R * tile + r) + n] = acc[r];
         __syncthreads();
-        if (tid < kGroupRows) {
+        if (tid < ROWS) {
             float sum = 0.f;
 #pragma unroll
             for (int k = 0; k < KS; ++k)
@@ -731,28 +832,32 @@ void gemv_mfma_kernel(Gemv2Args a) {
     }
 }
 
-template <int MEMBER, bool FLOOR, int MODE>
+template <int MEMBER, bool FLOOR, int MODE, int R>
 int launch_gemv_mfma(int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t st) {
-    const dim3 grid = MODE == kPairs ? dim3{a.out_features / kGroupRows, a.pairs_per_row, mats / a.pairs_per_row}
-                                     : dim3{a.out_features / kGroupRows, 1u, mats};
+    const uint32_t groups = a.out_features / (kGroupRows * R);
+    const dim3 grid = MODE == kPairs ? dim3{groups, a.pairs_per_row, mats / a.pairs_per_row} : dim3{groups, 1u, mats};
     const dim3 block4096{uint32_t(Gemv2Shape<MEMBER, 4096>::THREADS)}, block2048{uint32_t(Gemv2Shape<MEMBER, 2048>::THREADS)};
     if (n == 4096)
-        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 4096, FLOOR, MODE>), grid, block4096, 0, st, a);
+        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 4096, FLOOR, MODE, R>), grid, block4096, 0, st, a);
     else
-        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 2048, FLOOR, MODE>), grid, block2048, 0, st, a);
+        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 2048, FLOOR, MODE, R>), grid, block2048, 0, st, a);
     return record_launch(hipGetLastError());
 }
 
-template <bool FLOOR, int MODE>
+template <bool FLOOR, int MODE, int R>
 int launch_member(int member, int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t st) {
     switch (member) {
-        case IQK_MEMBER_IQ2_KS: return launch_gemv_mfma<IQ2_KS, FLOOR, MODE>(n, a, mats, st);
-        case IQK_MEMBER_IQ2_K: return launch_gemv_mfma<IQ2_K, FLOOR, MODE>(n, a, mats, st);
+        case IQK_MEMBER_IQ2_KS: return launch_gemv_mfma<IQ2_KS, FLOOR, MODE, R>(n, a, mats, st);
+        case IQK_MEMBER_IQ2_K: return launch_gemv_mfma<IQ2_K, FLOOR, MODE, R>(n, a, mats, st);
         default:
-            if constexpr (MODE == kPairs) return launch_gemv_mfma<IQ1_S_R4, FLOOR, MODE>(n, a, mats, st);
+            if constexpr (MODE == kPairs) return launch_gemv_mfma<IQ1_S_R4, FLOOR, MODE, R>(n, a, mats, st);
             return IQK_ERR_MEMBER;  // no sorted or union form for IQ1_S_R4
     }
 }
+
+// Dispatches of at least this many 32-row workgroups (four per CU slot of
+// a 1-token decode: 4 x 768) take two row blocks per wavefront.
+constexpr uint64_t kTwoRowMinGroups = 4 * 768;
 
 // Called by the GEMV entry points (after their argument checks) when
 // out_features is a multiple of the workgroup's 32 rows; returns -1 when this
@@ -782,11 +887,18 @@ int gemv_mfma_dispatch(bool floor, int member, int64_t n, int64_t out, int64_t n
     a.num_experts = uint32_t(num_experts);
     a.out_features = uint32_t(out);
     a.y = static_cast<uint16_t *>(y);
-    if (!toks)
-        return floor ? launch_member<true, kPairs>(member, n, a, mats, st) : launch_member<false, kPairs>(member, n, a, mats, st);
+    const bool two = out % (2 * kGroupRows) == 0 && uint64_t(mats) * uint64_t(out / kGroupRows) >= kTwoRowMinGroups;
+    if (!toks) {
+        if (floor)
+            return two ? launch_member<true, kPairs, 2>(member, n, a, mats, st)
+                       : launch_member<true, kPairs, 1>(member, n, a, mats, st);
+        return two ? launch_member<false, kPairs, 2>(member, n, a, mats, st)
+                   : launch_member<false, kPairs, 1>(member, n, a, mats, st);
+    }
     if (floor) return IQK_ERR_ARGUMENT;
-    return union_runs ? launch_member<false, kUnion>(member, n, a, mats, st)
-                      : launch_member<false, kSorted>(member, n, a, mats, st);
+    if (union_runs) return launch_member<false, kUnion, 1>(member, n, a, mats, st);
+    return two ? launch_member<false, kSorted, 2>(member, n, a, mats, st)
+               : launch_member<false, kSorted, 1>(member, n, a, mats, st);
 }
 
 }  // namespace iqk

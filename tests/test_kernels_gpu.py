@@ -139,6 +139,34 @@ def test_gemv_matches_a_float64_reference_per_pair_rows(device, member, n):
     _check_gemv(got, oracle.gemv_reference(ref, sel, x, 1), (member, n))
 
 
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+@pytest.mark.parametrize("n", kernels.SUPPORTED_IN_FEATURES)
+def test_gemv_large_dispatch_equals_small_dispatches(device, member, n):
+    """A dispatch of >= 4 x 768 row workgroups takes two 16-row blocks per
+    wavefront (shared activation reads); a row's arithmetic is the same, so
+    its outputs equal those of the same pairs in small one-block dispatches
+    bit for bit, and both meet the float64 gate.  Sorted form too (IQ2)."""
+    print(f"gemv large dispatch {member} n={n}", flush=True)
+    out, tokens, top_k = 256, 128, 3  # 384 pairs x 8 row workgroups = 3072
+    _, streams, ref = _case(member, n, wirepack.seed_for(member, n, "large"), device, out=out)
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal((tokens, n)).astype(np.float16)
+    sel = rng.integers(0, EXPERTS, size=tokens * top_k).astype(np.int32)
+    xt, st = torch.from_numpy(x).to(device), torch.from_numpy(sel).to(device)
+    big = kernels.gemv(member, xt, streams, st, top_k, EXPERTS, out).cpu().numpy()
+    chunk = 32  # 96 pairs x 8 = 768 row workgroups a call
+    small = np.concatenate([kernels.gemv(member, xt[t:t + chunk], streams, st[t * top_k:(t + chunk) * top_k], top_k,
+                                         EXPERTS, out).cpu().numpy() for t in range(0, tokens, chunk)])
+    assert np.array_equal(big.view(np.uint16), small.view(np.uint16)), member
+    _check_gemv(big, oracle.gemv_reference(ref, sel, x, top_k), (member, n))
+    if member in kernels.IQ2_MEMBERS:
+        order = np.argsort(sel, kind="stable")
+        toks = torch.from_numpy((order // top_k).astype(np.int32)).to(device)
+        ys = kernels.gemv_sorted(member, xt, streams, st[torch.from_numpy(order).to(device)], toks, EXPERTS,
+                                 out).cpu().numpy()
+        assert np.array_equal(ys.view(np.uint16), big[order].view(np.uint16)), member
+
+
 @pytest.mark.parametrize("n", kernels.SUPPORTED_IN_FEATURES)
 @pytest.mark.parametrize("out", (16, 48, 192))
 def test_gemv_iq2_ks_tiles(device, n, out):
