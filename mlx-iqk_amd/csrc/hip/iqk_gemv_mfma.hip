@@ -695,10 +695,10 @@ enum GemvMode : int {
 
 // R = 1: six wavefronts per SIMD, three workgroups of eight (N = 4096) or
 // six of four (N = 2048) per CU, so a 1-token routed decode's 768
-// workgroups are resident at once.  R = 2 (dispatches of many workgroups):
-// each wavefront takes 32 rows, two MFMA column blocks that share every A
-// read, so a workgroup stages its activations for 64 rows; four wavefronts
-// per SIMD.  kUnion keeps each lane's expanded weights in registers across
+// workgroups are resident at once.  R = 2 (IQ1_S_R4 dispatches of many
+// workgroups): each wavefront takes 32 rows, two MFMA column blocks that
+// share every A read, so a workgroup stages its activations for 64 rows;
+// five wavefronts per SIMD.  kUnion keeps each lane's expanded weights in registers across
 // its run (134-182 VGPRs): two or three wavefronts per SIMD, no spills.
 template <int MEMBER, int N, bool FLOOR, int MODE, int R>
 __global__ __launch_bounds__((Gemv2Shape<MEMBER, N>::THREADS))
@@ -855,8 +855,10 @@ int launch_member(int member, int64_t n, const Gemv2Args &a, uint32_t mats, hipS
     }
 }
 
-// Dispatches of at least this many 32-row workgroups (four per CU slot of
-// a 1-token decode: 4 x 768) take two row blocks per wavefront.
+// IQ1_S_R4 dispatches of at least this many 32-row workgroups (four times
+// the 768 of a 1-token decode) take two row blocks per wavefront.  The IQ2
+// members measured slower that way at 4 tokens and no faster at 8: they keep
+// one block.
 constexpr uint64_t kTwoRowMinGroups = 4 * 768;
 
 // Called by the GEMV entry points (after their argument checks) when
@@ -887,18 +889,18 @@ int gemv_mfma_dispatch(bool floor, int member, int64_t n, int64_t out, int64_t n
     a.num_experts = uint32_t(num_experts);
     a.out_features = uint32_t(out);
     a.y = static_cast<uint16_t *>(y);
-    const bool two = out % (2 * kGroupRows) == 0 && uint64_t(mats) * uint64_t(out / kGroupRows) >= kTwoRowMinGroups;
     if (!toks) {
-        if (floor)
-            return two ? launch_member<true, kPairs, 2>(member, n, a, mats, st)
-                       : launch_member<true, kPairs, 1>(member, n, a, mats, st);
-        return two ? launch_member<false, kPairs, 2>(member, n, a, mats, st)
-                   : launch_member<false, kPairs, 1>(member, n, a, mats, st);
+        const bool two = member == IQK_MEMBER_IQ1_S_R4 && out % (2 * kGroupRows) == 0 &&
+                         uint64_t(mats) * uint64_t(out / kGroupRows) >= kTwoRowMinGroups;
+        if (two)
+            return floor ? launch_gemv_mfma<IQ1_S_R4, true, kPairs, 2>(n, a, mats, st)
+                         : launch_gemv_mfma<IQ1_S_R4, false, kPairs, 2>(n, a, mats, st);
+        return floor ? launch_member<true, kPairs, 1>(member, n, a, mats, st)
+                     : launch_member<false, kPairs, 1>(member, n, a, mats, st);
     }
     if (floor) return IQK_ERR_ARGUMENT;
-    if (union_runs) return launch_member<false, kUnion, 1>(member, n, a, mats, st);
-    return two ? launch_member<false, kSorted, 2>(member, n, a, mats, st)
-               : launch_member<false, kSorted, 1>(member, n, a, mats, st);
+    return union_runs ? launch_member<false, kUnion, 1>(member, n, a, mats, st)
+                      : launch_member<false, kSorted, 1>(member, n, a, mats, st);
 }
 
 }  // namespace iqk

@@ -142,10 +142,11 @@ def test_gemv_matches_a_float64_reference_per_pair_rows(device, member, n):
 @pytest.mark.parametrize("member", fmt.MEMBERS)
 @pytest.mark.parametrize("n", kernels.SUPPORTED_IN_FEATURES)
 def test_gemv_large_dispatch_equals_small_dispatches(device, member, n):
-    """A dispatch of >= 4 x 768 row workgroups takes two 16-row blocks per
-    wavefront (shared activation reads); a row's arithmetic is the same, so
-    its outputs equal those of the same pairs in small one-block dispatches
-    bit for bit, and both meet the float64 gate.  Sorted form too (IQ2)."""
+    """An IQ1_S_R4 dispatch of >= 4 x 768 row workgroups takes two 16-row
+    blocks per wavefront (shared activation reads); a row's arithmetic is the
+    same, so its outputs equal those of the same pairs in small one-block
+    dispatches bit for bit, and meet the float64 gate.  The IQ2 members (one
+    block at any size) and their sorted form are held to the same."""
     print(f"gemv large dispatch {member} n={n}", flush=True)
     out, tokens, top_k = 256, 128, 3  # 384 pairs x 8 row workgroups = 3072
     _, streams, ref = _case(member, n, wirepack.seed_for(member, n, "large"), device, out=out)
