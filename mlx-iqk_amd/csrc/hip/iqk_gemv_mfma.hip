@@ -40,8 +40,13 @@
 //   sum(w x) = 2^-E (D0 + 2^8 D1 + 2^16 D2).  Each lane folds its own
 //   (row, sub-block) sums with the sub-block's scale.  Only the 12 lanes
 //   whose A row carries activations read LDS; the others hold zeros in
-//   registers for the whole kernel.  The partial sums of a row's lanes and
-//   wavefronts meet in LDS.
+//   registers for the whole kernel (IQ2_K, and the two-block form below:
+//   every lane reads, the others from a zero span).  The partial sums of a
+//   row's lanes and wavefronts meet in LDS.
+// * Two row blocks.  Large IQ1_S_R4 dispatches give each wavefront 32 rows
+//   (two 16-row blocks, R = 2) that share every A read, so a workgroup
+//   stages its activations once for 64 rows; the per-row arithmetic is the
+//   same as with one block, so results are identical bit for bit.
 //
 // The floor variants keep every global load and delete the decode.
 

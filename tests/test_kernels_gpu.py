@@ -153,15 +153,25 @@ def test_gemv_large_dispatch_equals_small_dispatches(device, member, n):
     rng = np.random.default_rng(23)
     x = rng.standard_normal((tokens, n)).astype(np.float16)
     sel = rng.integers(0, EXPERTS, size=tokens * top_k).astype(np.int32)
+    # an expert id beyond the stack and an infinite activation: NaN rows, the same in both forms
+    sel[40] = EXPERTS
+    x[70, n // 3] = np.inf
+    nan_pairs = np.zeros(tokens * top_k, dtype=bool)
+    nan_pairs[40] = True
+    nan_pairs[70 * top_k:71 * top_k] = True
     xt, st = torch.from_numpy(x).to(device), torch.from_numpy(sel).to(device)
     big = kernels.gemv(member, xt, streams, st, top_k, EXPERTS, out).cpu().numpy()
     chunk = 32  # 96 pairs x 8 = 768 row workgroups a call
     small = np.concatenate([kernels.gemv(member, xt[t:t + chunk], streams, st[t * top_k:(t + chunk) * top_k], top_k,
                                          EXPERTS, out).cpu().numpy() for t in range(0, tokens, chunk)])
     assert np.array_equal(big.view(np.uint16), small.view(np.uint16)), member
-    _check_gemv(big, oracle.gemv_reference(ref, sel, x, top_k), (member, n))
+    assert np.all(np.isnan(big[nan_pairs])) and not np.any(np.isnan(big[~nan_pairs])), member
+    keep = ~nan_pairs
+    with np.errstate(invalid="ignore", over="ignore"):  # the infinite token's rows, left out below
+        want = oracle.gemv_reference(ref, np.where(keep, sel, 0), x, top_k)
+    _check_gemv(big[keep], want[keep], (member, n))
     if member in kernels.IQ2_MEMBERS:
-        order = np.argsort(sel, kind="stable")
+        order = np.argsort(sel, kind="stable")  # the invalid id sorts last
         toks = torch.from_numpy((order // top_k).astype(np.int32)).to(device)
         ys = kernels.gemv_sorted(member, xt, streams, st[torch.from_numpy(order).to(device)], toks, EXPERTS,
                                  out).cpu().numpy()
