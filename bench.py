@@ -10,8 +10,10 @@ steps replay as one captured HIP graph between two synchronisations.
 
 Also reported, outside the timed region: every member's decode against its
 own deleted-decode floor (IQ2_KS and IQ1_S_R4 at 1 token, IQ2_K at 8 tokens),
-the dequant producer against its floor, the Zipf(1.1) mixed-member prefill
-(producer GB/s, grouped-GEMM TFLOP/s and MFMA utilisation), and the
+the dequant producer against its floor and its row-range form, the Zipf(1.1)
+mixed-member prefill (producer GB/s, grouped-GEMM and fused-GEMM TFLOP/s and
+MFMA utilisation), the sorted and union decode forms on uniform multi-token
+routing, the GPU wire ingest (pack), the host quantizers, and the
 reference's CPU dequantizer + float32 matmul on a bounded sample of the
 headline step.
 
@@ -60,7 +62,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--rounds", type=int, default=5, help="alternated decode/floor rounds per cell")
     ap.add_argument("--block", type=int, default=200, help="dispatches per captured graph in a cell")
     ap.add_argument("--distinct", type=int, default=2, help="distinct quantized experts per projection")
-    ap.add_argument("--cells", default="iq2_ks,iq2_k,iq1_s_r4,dequant,prefill,pack")
+    ap.add_argument("--cells", default="iq2_ks,iq2_k,iq1_s_r4,dequant,prefill,pack,verify,quantize")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="CPU baseline sample budget (half on one thread, half on every core)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -261,11 +263,20 @@ def dequant_cell(torch, device, member: str, args, seed: int):
 
         def launch(i, floor=False):
             return lambda: kernels.dequant(member, parts[i % len(parts)], chunk, out, n, floor=floor, out=w)
+        # the row-range form: the middle half of each expert's rows
+        r0, nr = out // 4, out // 2
+        wr = torch.empty((chunk, nr, n), dtype=torch.float16, device=device)
+
+        def launch_range(i):
+            return lambda: kernels.dequant(member, parts[i % len(parts)], chunk, out, n, row_start=r0, rows=nr, out=wr)
         arms = {"decode": Arm(torch, [launch(i) for i in range(B)], "decode"),
-                "floor": Arm(torch, [launch(i, True) for i in range(B)], "floor")}
+                "floor": Arm(torch, [launch(i, True) for i in range(B)], "floor"),
+                "range": Arm(torch, [launch_range(i) for i in range(B)], "range")}
         r = alternate(arms, args.rounds)
         read = chunk * out * fmt.ik_row_bytes(member, n)
         written = chunk * out * n * 2
+        r["range"]["rows"] = [r0, r0 + nr]
+        r["range"]["gb_per_s"] = round((read + written) / 2 / (r["range"]["median_us"] * 1e-6) / 1e9, 1)
         r.update({"experts": chunk, "read_bytes": read, "written_bytes": written,
                   "x_floor": round(r["decode"]["median_us"] / r["floor"]["median_us"], 4)})
         for arm in ("decode", "floor"):
@@ -273,8 +284,9 @@ def dequant_cell(torch, device, member: str, args, seed: int):
             r[arm]["frac_of_8tbps"] = round(r[arm]["gb_per_s"] / HBM_PEAK_GBS, 4)
         res[name] = r
         log(f"  decode {r['decode']['median_us']:9.2f} us ({r['decode']['gb_per_s']:7.1f} GB/s)  floor "
-            f"{r['floor']['median_us']:9.2f} us  x{r['x_floor']:.3f}")
-        del arms, st, parts, w
+            f"{r['floor']['median_us']:9.2f} us  x{r['x_floor']:.3f}  half-range {r['range']['median_us']:.2f} us "
+            f"({r['range']['gb_per_s']} GB/s)")
+        del arms, st, parts, w, wr
         torch.cuda.empty_cache()
     return res
 
@@ -380,6 +392,100 @@ def prefill_cell(torch, device, args, seed: int):
     res["mfma_utilisation"] = round(res["gemm_tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
     res["fused_tflops"] = round(tot_flop / (tot_fused * 1e-6) / 1e12, 2)
     res["fused_mfma_utilisation"] = round(res["fused_tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
+    return res
+
+
+def verify_cell(torch, device, args, seed: int):
+    """Multi-token decode with uniform top-6 routing per token (experts repeat
+    across tokens): the pair GEMV against the expert-sorted and the union forms
+    (one read of each distinct expert per run), IQ2_K on the gate geometry
+    [2048x4096] of a 256-expert stack.  GB/s counts each distinct expert once."""
+    from mlx_iqk_amd import format as fmt
+    from mlx_iqk_amd import kernels, synth
+
+    member, (out, n) = "iq2_k", GU
+    stack = synth.expert_stack(member, EXPERTS, out, n, seed, device, args.distinct, "verify")
+    rb = fmt.ik_row_bytes(member, n)
+    rng = np.random.default_rng(seed)
+    res = {"member": member, "geometry": [out, n]}
+    for tokens in (8, 32):
+        variants = 16
+        V = []
+        for _ in range(variants):
+            idx = np.stack([rng.choice(EXPERTS, TOP_K, replace=False) for _ in range(tokens)]).astype(np.int32)
+            flat = idx.reshape(-1)
+            order = np.argsort(flat, kind="stable")
+            V.append({"x": torch.randn(tokens, n, device=device).to(torch.float16),
+                      "sel": torch.from_numpy(flat).to(device),
+                      "sorted": torch.from_numpy(flat[order]).to(device),
+                      "toks": torch.from_numpy((order // TOP_K).astype(np.int32)).to(device),
+                      "distinct": int(np.unique(flat).size),
+                      "y": torch.empty(flat.size, out, dtype=torch.float16, device=device)})
+        # the three forms agree bit for bit (sorted/union rows are the pair rows, reordered)
+        v = V[0]
+        yp = kernels.gemv(member, v["x"], stack, v["sel"], TOP_K, EXPERTS, out).cpu().numpy()
+        order = np.argsort(v["sel"].cpu().numpy(), kind="stable")
+        for union in (False, True):
+            ys = kernels.gemv_sorted(member, v["x"], stack, v["sorted"], v["toks"], EXPERTS, out,
+                                     union=union).cpu().numpy()
+            if not np.array_equal(ys.view(np.uint16), yp[order].view(np.uint16)):
+                raise SystemExit(f"verify cell: the {'union' if union else 'sorted'} form differs from the pair form")
+
+        def launch(i, mode):
+            v = V[i % variants]
+            if mode in ("pairs", "floor"):
+                return lambda: kernels.gemv(member, v["x"], stack, v["sel"], TOP_K, EXPERTS, out,
+                                            floor=mode == "floor", out=v["y"])
+            return lambda: kernels.gemv_sorted(member, v["x"], stack, v["sorted"], v["toks"], EXPERTS, out,
+                                               union=mode == "union", out=v["y"])
+        arms = {mode: Arm(torch, [launch(i, mode) for i in range(variants)], mode)
+                for mode in ("pairs", "floor", "sorted", "union")}
+        r = alternate(arms, args.rounds)
+        distinct = statistics.mean(v["distinct"] for v in V)
+        nbytes = distinct * out * rb
+        cell = {"pairs": tokens * TOP_K, "distinct_experts_mean": round(distinct, 1),
+                "distinct_bytes": round(nbytes)}
+        for mode in ("pairs", "floor", "sorted", "union"):
+            cell[mode] = {"median_us": r[mode]["median_us"],
+                          "gb_per_s_distinct": round(nbytes / (r[mode]["median_us"] * 1e-6) / 1e9, 1)}
+        cell["union_speedup_over_pairs"] = round(r["pairs"]["median_us"] / r["union"]["median_us"], 3)
+        res[f"tokens_{tokens}"] = cell
+        log(f"[verify {member} x{tokens}] {tokens * TOP_K} pairs, {distinct:.1f} distinct experts: "
+            + "  ".join(f"{m} {r[m]['median_us']:.1f} us" for m in ("pairs", "floor", "sorted", "union")))
+        del arms, V
+        torch.cuda.empty_cache()
+    del stack
+    torch.cuda.empty_cache()
+    return res
+
+
+def quantize_cell(args, seed: int):
+    """The package codec's quantizers on the host: rows of 4096 from N(0, 0.02) with a
+    U(0.1, 1) imatrix, at the default worker count and on one thread (a bounded
+    sample; the IQ1_S_R4 grid-neighbour tables are built before timing)."""
+    from mlx_iqk_amd import codec
+    from mlx_iqk_amd import format as fmt
+
+    rng = np.random.default_rng(seed)
+    n = GU[1]
+    w = rng.normal(0.0, 0.02, (256, n)).astype(np.float32)
+    im = rng.uniform(0.1, 1.0, n).astype(np.float32)
+    res = {"in_features": n, "threads_default": codec.threads()}
+    for member in ("iq2_ks", "iq2_k", "iq1_s_r4"):
+        codec.quantize(member, w[:4], im)  # warm-up (tables)
+        cell = {}
+        for label, threads in (("default", 0), ("one_thread", 1)):
+            codec.set_threads(threads)
+            rows = 256 if threads == 0 else 64
+            t0 = time.perf_counter()
+            codec.quantize(member, w[:rows], im)
+            dt = time.perf_counter() - t0
+            cell[label] = {"rows": rows, "rows_per_s": round(rows / dt, 1),
+                           "wire_mb_per_s": round(rows * fmt.ik_row_bytes(member, n) / dt / 1e6, 2)}
+        codec.set_threads(0)
+        res[member] = cell
+        log(f"[quantize {member}] {cell['default']['rows_per_s']} rows/s on {res['threads_default']} threads, "
+            f"{cell['one_thread']['rows_per_s']} on one")
     return res
 
 
@@ -548,6 +654,10 @@ def main() -> int:
         results["prefill"] = prefill_cell(torch, device, args, seed=23)
     if "pack" in cells:
         results["pack"] = pack_cell(torch, device, args, seed=29)
+    if "verify" in cells:
+        results["verify"] = verify_cell(torch, device, args, seed=31)
+    if "quantize" in cells:
+        results["quantize"] = quantize_cell(args, seed=37)
     base = None if args.no_cpu else cpu_baseline(args.cpu_seconds, args.distinct, seed=11)
 
     gu = results["iq2_ks"]["cells"]["gate_up"]

@@ -159,6 +159,8 @@ __device__ __forceinline__ uint32_t hi16_x8(uint32_t v) {
 __device__ __forceinline__ void pin(float &v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void pin(uint32_t &v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void pin(int &v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(uint2_t &v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(uint4_t &v) { asm volatile("" : "+v"(v)); }
 
 // Two IQ1_S_R4 grid entries (the low and high 16 bits of e; 2-bit code c
 // at bit 2k for weight k, g = c - 1) as int8 weights 8g + 1, eight bytes an
@@ -332,6 +334,17 @@ struct LaneIq2ks {
         for (uint32_t s = 0; s < 4; ++s) q[s] = load_u4(bytes(a.s0) + (row * (N / 4) + 256 * kq + 64 * s + 16 * g));
     }
 
+    // The stream words as if reloaded: a loop over pairs then expands them
+    // anew each pair instead of keeping the expanded weights live.
+    __device__ __forceinline__ void launder() {
+        pin(sc);
+        pin(hb);
+        pin(ab);
+        pin(dvb);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) pin(q[s]);
+    }
+
     __device__ __forceinline__ uint32_t hash() const {
         uint32_t h = 59u * (sc.x + sc.y + sc.z + sc.w) + 61u * hb + 71u * ab + 67u * dvb;
 #pragma unroll
@@ -342,7 +355,7 @@ struct LaneIq2ks {
     // Sub-blocks 8s+2g+h (32 weights, words 2h, 2h+1 of q[s]) of R rows, one
     // lane instance each, which share every A read; sbs / nsbs: 2^-E and
     // -16 x 2^-E of each 32-element block.
-    template <int R>
+    template <int R, bool EARLY>
     __device__ __forceinline__ static void decode(const LaneIq2ks (&ln)[R], const uint8_t *abase, bool data,
                                                   const float *sbs, const float *nsbs, int g, float (&out)[R]) {
         // Scale index x 2^-E and alphabet pool of sub-blocks 8s+2g+h, formed
@@ -358,9 +371,9 @@ struct LaneIq2ks {
         const uint32_t selg = (g2 | (g2 << 16)) + 0x04000400u;  // bytes g, 4+g, g, 4+g
         float fac[R][4][2];
         uint32_t pool[R][4][2], idx4[R];
-        // Super-block s's factors and pools.  One row block forms them all
-        // before the first code word; two form each just before its MFMAs
-        // (the registers of all four would cost a wavefront per SIMD).
+        // Super-block s's factors and pools: all before the first code word
+        // (EARLY), or each just before its MFMAs (the registers of all four
+        // would cost a wavefront per SIMD).
         const auto prep = [&](int s) {
             const int sp = s >> 1, t = s & 1;
 #pragma unroll
@@ -383,7 +396,7 @@ struct LaneIq2ks {
                 }
             }
         };
-        if constexpr (R == 1) {
+        if constexpr (EARLY) {
 #pragma unroll
             for (int s = 0; s < 4; ++s) prep(s);
         }
@@ -395,7 +408,7 @@ struct LaneIq2ks {
         for (int s = 0; s <= 4; ++s) {
             int4_t D[R][2];
             if (s < 4) {
-                if constexpr (R > 1) prep(s);
+                if constexpr (!EARLY) prep(s);
                 read_a(A, abase + 256 * s, data);
 #pragma unroll
                 for (int r = 0; r < R; ++r)
@@ -439,6 +452,16 @@ struct LaneIq2k {
         for (uint32_t s = 0; s < 4; ++s) q[s] = load_u4(bytes(a.s0) + (row * (N / 4) + 256 * kq + 64 * s + 16 * g));
     }
 
+    // The stream words as if reloaded (see LaneIq2ks::launder).
+    __device__ __forceinline__ void launder() {
+        pin(sc0);
+        pin(sc1);
+        pin(ex);
+        pin(dv);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) pin(q[s]);
+    }
+
     __device__ __forceinline__ uint32_t hash() const {
         uint32_t h = 59u * (sc0.x + sc0.y + sc0.z + sc0.w + sc1.x + sc1.y + sc1.z + sc1.w) +
                      71u * (ex.x + ex.y) + 67u * (dv.x + dv.y);
@@ -456,7 +479,7 @@ struct LaneIq2k {
     // part idx * off * sum(f) takes one fma per word from the word's integer
     // activation sum fw.  A lane folds once per super-block.
     // R rows, one lane instance each, share every A read.
-    template <int R>
+    template <int R, bool EARLY>
     __device__ __forceinline__ static void decode(const LaneIq2k (&ln)[R], const uint8_t *abase, const float *sbs,
                                                   const float *fw, const uint2_t *ktab, int g, float (&out)[R]) {
         // This lane's scale word of super-block s is u16 g of the pair
@@ -478,9 +501,9 @@ struct LaneIq2k {
             exg[r][0] = ln[r].ex.x >> exs;
             exg[r][1] = ln[r].ex.y >> exs;
         }
-        // Super-block s's factors and pools.  One row block forms them all
-        // before the first code word; two form each just before its MFMAs
-        // (the registers of all four would cost a wavefront per SIMD).
+        // Super-block s's factors and pools: all before the first code word
+        // (EARLY), or each just before its MFMAs (the registers of all four
+        // would cost a wavefront per SIMD).
         const auto prep = [&](int s) {
             const float4 fwv = *reinterpret_cast<const float4 *>(fw + 16 * s + 4 * g);
 #pragma unroll
@@ -504,7 +527,7 @@ struct LaneIq2k {
                 }
             }
         };
-        if constexpr (R == 1) {
+        if constexpr (EARLY) {
 #pragma unroll
             for (int s = 0; s < 4; ++s) prep(s);
         }
@@ -518,7 +541,7 @@ struct LaneIq2k {
 #pragma unroll
             for (int r = 0; r < R; ++r) W[r] = int4_t{0, 0, 0, 0};
             if (s < 4) {
-                if constexpr (R > 1) prep(s);
+                if constexpr (!EARLY) prep(s);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int4_t a = read_a_all(abase + 256 * s + 16 * j);
@@ -597,15 +620,15 @@ struct LaneIq1s {
     // 8g - 1, which takes 2 sum(f) off its digit sum.  fsum2: 2 sum(f) of
     // each 32-element block.
     // R rows, one lane instance each, share every A read.
-    template <int R>
+    template <int R, bool EARLY>
     __device__ __forceinline__ static void decode(const LaneIq1s (&ln)[R], const uint8_t *abase, bool data,
                                                   const float *sbs, const int *fsum2, const uint2_t *b8, int g,
                                                   float (&out)[R]) {
         // Each block's scale x 2^-E and its negative-shift correction
         // 2 sum(f) (or 0); 2s + 1 of the two blocks of a qh dword lands in
-        // its bytes 0 and 2 in two ops.  One row block forms them all before
-        // the first index byte; two form each pair of blocks just before its
-        // MFMAs (the registers of all would cost a wavefront per SIMD).
+        // its bytes 0 and 2 in two ops.  All are formed before the first
+        // index byte (EARLY), or each pair of blocks just before its MFMAs
+        // (the registers of all would cost a wavefront per SIMD).
         float fac[R][4 * NI];
         int corr[R][4 * NI];
         const auto prep = [&](int i, int bp) {  // blocks 4i + 2bp, +1
@@ -625,7 +648,7 @@ struct LaneIq1s {
                 }
             }
         };
-        if constexpr (R == 1) {
+        if constexpr (EARLY) {
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
                 prep(i, 0);
@@ -643,7 +666,7 @@ struct LaneIq1s {
             if (c < 4 * NI) {
                 const int i = c >> 2, b = c & 3;
                 if ((b & 1) == 0) {  // blocks b, b+1
-                    if constexpr (R > 1) prep(i, b >> 1);
+                    if constexpr (!EARLY) prep(i, b >> 1);
                     read_a(A, abase + 512 * i + 32 * b, data);
                 }
 #pragma unroll
@@ -703,11 +726,11 @@ enum GemvMode : int {
 // workgroups are resident at once.  R = 2 (IQ1_S_R4 dispatches of many
 // workgroups): each wavefront takes 32 rows, two MFMA column blocks that
 // share every A read, so a workgroup stages its activations for 64 rows;
-// five wavefronts per SIMD.  kUnion keeps each lane's expanded weights in registers across
-// its run (134-182 VGPRs): two or three wavefronts per SIMD, no spills.
+// five wavefronts per SIMD.  kUnion re-expands a lane's stream words for
+// each pair of its run (the words are read once); five wavefronts per SIMD.
 template <int MEMBER, int N, bool FLOOR, int MODE, int R>
 __global__ __launch_bounds__((Gemv2Shape<MEMBER, N>::THREADS))
-__attribute__((amdgpu_waves_per_eu(MODE == kUnion ? 2 : R == 2 ? 5 : 6)))
+__attribute__((amdgpu_waves_per_eu(MODE == kUnion || R == 2 ? 5 : 6)))
 void gemv_mfma_kernel(Gemv2Args a) {
     using S = Gemv2Shape<MEMBER, N>;
     constexpr int KS = S::KS;
@@ -724,11 +747,27 @@ void gemv_mfma_kernel(Gemv2Args a) {
 
     // The run of pairs this workgroup serves: one pair, or for kUnion every
     // pair of a run of equal ids (workgroups of the run's other pairs exit).
+    // The ids around m0 are read as one batch of independent loads (one
+    // latency, not a chain of them); a run longer than the batch reads on.
     uint32_t run = 1;
     if constexpr (MODE == kUnion) {
-        const uint32_t e_first = a.sel[m0];
-        if (m0 > 0 && a.sel[m0 - 1] == e_first) return;  // uniform: not the run's first pair
-        while (m0 + run < a.mats && a.sel[m0 + run] == e_first) ++run;
+        constexpr int kScan = 8;
+        uint32_t ids[kScan + 1];  // sel[m0 - 1 .. m0 + kScan - 1], where they exist
+#pragma unroll
+        for (int i = 0; i <= kScan; ++i) {
+            const uint32_t m = m0 + uint32_t(i) - 1u;
+            ids[i] = (i > 0 || m0 > 0) && m < a.mats ? a.sel[m] : 0u;
+        }
+        const uint32_t e_first = ids[1];
+        if (m0 > 0 && ids[0] == e_first) return;  // uniform: not the run's first pair
+        bool open = true;
+#pragma unroll
+        for (int i = 2; i <= kScan; ++i) {
+            open = open && m0 + uint32_t(i) - 1u < a.mats && ids[i] == e_first;
+            run += open ? 1u : 0u;
+        }
+        if (open)
+            while (m0 + run < a.mats && a.sel[m0 + run] == e_first) ++run;
     }
     // Activation row of pair m; a row beyond x reads row 0 and yields NaN.
     const auto x_row = [&](uint32_t m) -> uint32_t {
@@ -775,6 +814,12 @@ void gemv_mfma_kernel(Gemv2Args a) {
             tok = x_row(m);
             x_ok = tok < a.n_x_rows;
             load_x(x_ok ? tok : 0u, xv);
+            // expand them anew (not for the first pair: pinning a word still
+            // in flight would wait for every word up front)
+            if constexpr (MODE == kUnion) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) lane[r].launder();
+            }
         }
         float acc[R];
         if constexpr (FLOOR) {
@@ -808,12 +853,16 @@ void gemv_mfma_kernel(Gemv2Args a) {
             const bool reads = data || !MASKED;  // lanes that read A
             const float *sbs = sm.sbs + (S::WK / 32) * kq;
             using Lane = LaneOf<MEMBER, N>;
+            // the prologue of every super-block before the first code word,
+            // or (two row blocks, or a loop over a run's pairs) each just
+            // before its MFMAs: registers for a wavefront per SIMD
+            constexpr bool EARLY = R == 1 && MODE != kUnion;
             if constexpr (IQ1)
-                Lane::template decode<R>(lane, abase, reads, sbs, sm.fsum + (S::WK / 32) * kq, sm.b8, g, acc);
+                Lane::template decode<R, EARLY>(lane, abase, reads, sbs, sm.fsum + (S::WK / 32) * kq, sm.b8, g, acc);
             else if constexpr (MEMBER == IQ2_KS)
-                Lane::template decode<R>(lane, abase, reads, sbs, sm.nsbs + (S::WK / 32) * kq, g, acc);
+                Lane::template decode<R, EARLY>(lane, abase, reads, sbs, sm.nsbs + (S::WK / 32) * kq, g, acc);
             else
-                Lane::template decode<R>(lane, abase, sm.sbs + (S::WK / 64) * kq, sm.fw + (S::WK / 16) * kq,
+                Lane::template decode<R, EARLY>(lane, abase, sm.sbs + (S::WK / 64) * kq, sm.fw + (S::WK / 16) * kq,
                                          sm.ktab, g, acc);
         }
         // Partials of the row's lanes and wavefronts: wave 0 sums them after
@@ -830,10 +879,12 @@ void gemv_mfma_kernel(Gemv2Args a) {
             a.y[size_t(m) * a.out_features + rowg + tid] = valid && x_ok ? uint16_t(float_to_half_bits(sum)) : kHalfNaN;
         }
     };
+    // The run's first pair is straight-line code, as in the other forms, so
+    // its staging waits for the activations only, not for the stream words
+    // (inside a loop the compiler waits for every load first).
+    contract(0);
     if constexpr (MODE == kUnion) {
-        for (uint32_t q = 0; q < run; ++q) contract(q);
-    } else {
-        contract(0);
+        for (uint32_t q = 1; q < run; ++q) contract(q);
     }
 }
 

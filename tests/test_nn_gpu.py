@@ -14,6 +14,7 @@ import torch
 
 import wirepack
 from mlx_iqk_amd import format as fmt
+from mlx_iqk_amd import kernels
 from mlx_iqk_amd.iq1grid import grid_values
 from mlx_iqk_amd.nn import (DECODE_MAT_LIMIT, IqkKernelError, IqkRuntimeError, IqkSwitchLinear, grid_table,
                              member_table, value_table)
@@ -279,6 +280,28 @@ def test_union_gemv_covers_the_run_extremes(device, member):
         for fn in (module.gemv_union, module.gemv_sorted):
             got = fn(x, sorted_ids, toks)[inv].reshape(pair.shape)
             assert np.array_equal(_bits(got), _bits(pair))
+
+
+@pytest.mark.parametrize("member", IQ2)
+def test_union_runs_past_the_id_batch_and_invalid_ids(device, member):
+    """Runs longer than the kernel's batch of eight ids, one ending on it, and
+    ids beyond the stack (0xFFFFFFFF first, the stack size last): the union
+    form equals the sorted form bit for bit, and invalid ids give NaN rows."""
+    n = 2048
+    module, _ = _module(member, n, 97, device)
+    runs = [(0xFFFFFFFF, 1), (0, 10), (1, 1), (2, 7), (3, 8), (1, 3), (EXPERTS, 3)]
+    ids = np.concatenate([np.full(k, e, dtype=np.uint32) for e, k in runs])
+    rng = np.random.default_rng(101)
+    rows = 9
+    x = torch.from_numpy(rng.standard_normal((rows, n)).astype(np.float16)).to(device)
+    toks = torch.from_numpy(rng.integers(0, rows, size=ids.size).astype(np.int32)).to(device)
+    sel = torch.from_numpy(ids.view(np.int32)).to(device)
+    ys, yu = (kernels.gemv_sorted(member, x, module._streams(), sel, toks, EXPERTS, OUT, union=u)
+              for u in (False, True))
+    assert np.array_equal(_bits(yu), _bits(ys))
+    bad = ids >= EXPERTS
+    y = yu.float().cpu().numpy()
+    assert np.all(np.isnan(y[bad])) and not np.any(np.isnan(y[~bad]))
 
 
 @pytest.mark.parametrize("member", IQ2)
