@@ -93,7 +93,10 @@ int iqk_gemv_sorted(int member, int64_t in_features, int64_t out_features, int64
 // src/mlx_iqk/kernels.py:484-578, 834-853, src/mlx_iqk/nn.py:301-333): the
 // workgroup of a run's first pair computes every pair of the run from one
 // read of the expert's rows.  Arguments, output and refusals as
-// iqk_gemv_sorted, and bit-identical to it.
+// iqk_gemv_sorted, and bit-identical to it.  The run's pairs are computed one
+// after another, so with short runs (routing that rarely repeats an expert)
+// iqk_gemv_sorted is faster: its run's workgroups run side by side and share
+// the expert's bytes through L2.
 int iqk_gemv_union(int member, int64_t in_features, int64_t out_features, int64_t num_experts,
                    const void *x, int64_t n_x_rows, const void *const *streams, int n_streams,
                    const uint32_t *sorted_ids, const uint32_t *toks, uint32_t mats,

@@ -215,7 +215,9 @@ class IqkSwitchLinear(torch.nn.Module):
         equal adjacent ids: the multi-token verify shape, where several pairs
         select one expert (reference: src/mlx_iqk/nn.py:301-333).  Output and
         arithmetic identical to :meth:`gemv_sorted`; the caller applies the
-        inverse permutation."""
+        inverse permutation.  A run's pairs are computed one after another,
+        so for routing that rarely repeats an expert :meth:`gemv_sorted` is
+        the faster of the two."""
         xt, sel, tok = self._sorted_operands(x, sorted_ids, toks)
         return kernels.gemv_sorted(self.member, xt, self._streams(), sel, tok, self.num_experts,
                                    self.out_features, union=True)
