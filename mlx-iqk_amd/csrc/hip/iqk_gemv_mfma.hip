@@ -139,19 +139,14 @@ __device__ __forceinline__ uint32_t half_row_mirror(uint32_t v) {
 
 __device__ __forceinline__ int digits_sum(int4_t d) { return (((d.z << 8) + d.y) << 8) + d.x; }
 
-// 8 x the low / high 16 bits of v: one SDWA shift each.
-__device__ __forceinline__ uint32_t lo16_x8(uint32_t v) {
-    uint32_t r;
-    asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_0"
-        : "=v"(r) : "v"(v));
-    return r;
-}
-__device__ __forceinline__ uint32_t hi16_x8(uint32_t v) {
-    uint32_t r;
-    asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_1"
-        : "=v"(r) : "v"(v));
-    return r;
-}
+// 8 x the low / high 16 bits of v.  Plain code, not inline asm: the
+// compiler must see every instruction that writes a register, because a
+// register whose last writer was an MFMA still in flight (an unused dword of
+// its result) may be handed to the next value, and only the compiler's
+// hazard pass inserts the wait that keeps the MFMA's late write from landing
+// on top of it.
+__device__ __forceinline__ uint32_t lo16_x8(uint32_t v) { return (v & 0xffffu) << 3; }
+__device__ __forceinline__ uint32_t hi16_x8(uint32_t v) { return (v >> 16) << 3; }
 
 // Keeps a value computed where it stands.  The masked A reads split a decode
 // into one block per super-block, and without a use in its own block each
