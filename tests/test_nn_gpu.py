@@ -475,6 +475,33 @@ def test_fused_prefill_serves_partial_row_blocks_and_several_rows_per_pair(devic
     assert _rel(fused, want) < 3e-3
 
 
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+@pytest.mark.parametrize("n", (2048, 4096))
+def test_fused_prefill_experts_of_many_tiles(device, member, n):
+    """Experts that span several 64-slot M-tiles, full and partial: sizes 300
+    (four full tiles and a 44-slot one), 128 (two full), 200 (three full and
+    an 8-slot one), 129 (two full and a one-slot one), 64, 5, 1 and 0.  Both
+    routes meet the float64 gate and agree with each other, and row ranges
+    concatenate to the unsplit call bit for bit."""
+    print(f"fused prefill many tiles {member} n={n}", flush=True)
+    module, ref = _module(member, n, wirepack.seed_for(member, n, "wide"), device)
+    sizes = [300, 128, 200, 1, 0, 5, 64, 129]
+    assert len(sizes) == EXPERTS
+    idx = np.concatenate([np.full(c, e) for e, c in enumerate(sizes)]).astype(np.int32).reshape(-1, 1)
+    rng = np.random.default_rng(131)
+    x = rng.standard_normal((idx.shape[0], 1, 1, n)).astype(np.float16)
+    xt, it = torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device)
+    fused, producer = _both_routes(module, xt, it, sorted_indices=True)
+    want = oracle.prefill_reference(ref, x, idx)
+    assert _rel(fused, want) < 3e-3 and _rel(producer, want) < 3e-3
+    diff = (fused.float() - producer.float()).abs().max().item()
+    assert diff <= 2e-3 * producer.float().abs().max().item()
+    half = OUT // 2
+    parts = torch.cat([module.sorted_matmul_range(xt, it, 0, half),
+                       module.sorted_matmul_range(xt, it, half, half)], dim=-1)
+    assert np.array_equal(_bits(parts), _bits(fused))
+
+
 @pytest.mark.parametrize("member", ("iq2_ks", "iq1_s_r4"))
 def test_fused_prefill_at_the_routed_geometry(device, member):
     """256 experts at the gate/up geometry, a Zipf-skewed 64-token top-6
