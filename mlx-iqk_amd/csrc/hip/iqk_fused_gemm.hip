@@ -114,7 +114,7 @@ __device__ __forceinline__ void copy_plane(const uint8_t *src, int rows, int byt
 // its 64 weights: IQ2_KS sub-blocks 4s + 2kg + h (two words each), IQ2_K
 // sub-blocks 8s + 4kg + w (one word each).  Same f32 chain as the producer.
 template <int MEMBER, int K>
-__device__ __forceinline__ void fused_pools(const FusedScales<MEMBER, K> &sc, int row, int s, int kg, float d,
+__device__ __forceinline__ void fused_pools(const FusedScales<MEMBER, K> &sc, int row, int s, int kg, _Float16 d,
                                             Pool *p) {
     using S = FusedScales<MEMBER, K>;
     if constexpr (MEMBER == IQ2_KS) {
@@ -126,22 +126,18 @@ __device__ __forceinline__ void fused_pools(const FusedScales<MEMBER, K> &sc, in
         for (int h = 0; h < 2; ++h) {
             const int idx = int(((scl >> (4 * h)) & 15u) | (((hb >> (bit + h)) & 1u) << 4)) - 16;
             const bool alpha = (ab >> (bit + h)) & 1u;
-            const float dl = d * float(idx);
-            p[2 * h] = make_pool(dl, alpha ? -26.f : -31.f, alpha ? -8.f : -13.f, alpha ? 6.f : 1.f,
-                                 alpha ? 22.f : 17.f);
+            p[2 * h] = make_pool_h(d, _Float16(short(idx)), iq2_pair(alpha, 0), iq2_pair(alpha, 1));
             p[2 * h + 1] = p[2 * h];
         }
     } else {
         const uint32_t scw = *reinterpret_cast<const uint16_t *>(sc.scl + row * S::SCL_S + 2 * (2 * s + kg));
         const uint32_t ab = sc.ex[row * S::EX_S + s] >> (4 * kg);
-        const float dd = half_bits_to_float(*reinterpret_cast<const uint16_t *>(sc.dv + row * S::DV_S + 2 * (s >> 1)));
+        const _Float16 dd = half_of_bits(*reinterpret_cast<const uint16_t *>(sc.dv + row * S::DV_S + 2 * (s >> 1)));
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
             const int idx = int((scw >> (4 * w)) & 15u) - 8;
             const bool alpha = (ab >> w) & 1u;
-            const float dl = dd * float(idx);
-            p[w] = make_pool(dl, alpha ? -26.f : -31.f, alpha ? -8.f : -13.f, alpha ? 6.f : 1.f,
-                             alpha ? 22.f : 17.f);
+            p[w] = make_pool_h(dd, _Float16(short(idx)), iq2_pair(alpha, 0), iq2_pair(alpha, 1));
         }
     }
 }
@@ -150,11 +146,11 @@ __device__ __forceinline__ void fused_pools(const FusedScales<MEMBER, K> &sc, in
 // word b of q.z).  Pools p[2b], p[2b+1] are block b's (dl = d (2s+1), values
 // g + shift, as the producer), and word 2b+t holds the grid codes of the
 // block's 8-weight groups 2t and 2t+1.
-__device__ __forceinline__ void fused_iq1(uint4_t q, const uint16_t *grid, float d, Pool *p, uint32_t *words) {
+__device__ __forceinline__ void fused_iq1(uint4_t q, const uint16_t *grid, _Float16 d, Pool *p, uint32_t *words) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
         const uint32_t qw = q[b], h = (q.z >> (16 * b)) & 0xffffu;
-        const float dl = d * float(int(2 * ((h >> 12) & 7u) + 1));
+        const float dl = float(d) * float(int(2 * ((h >> 12) & 7u) + 1));
         const float sh = (h & 0x8000u) ? -0.125f : 0.125f;
         p[2 * b] = make_pool(dl, -1.f + sh, 0.f + sh, 1.f + sh, 2.f + sh);  // grid field 3 never occurs
         p[2 * b + 1] = p[2 * b];
@@ -261,11 +257,11 @@ void fused_gemm_kernel(FusedArgs a) {
     // row scale: IQ2_KS from LDS (rows past out_features read LDS junk, never
     // stored), IQ1_S_R4 from its stream (an in-bounds row); IQ2_K's are per
     // super-block
-    float d = 0.f;
+    _Float16 d = 0.f16;
     if constexpr (MEMBER == IQ2_KS)
-        d = half_bits_to_float(*reinterpret_cast<const uint16_t *>(sc.dv + lrow * S::DV_S));
+        d = half_of_bits(*reinterpret_cast<const uint16_t *>(sc.dv + lrow * S::DV_S));
     else if constexpr (IQ1)
-        d = half_bits_to_float(static_cast<const uint16_t *>(a.s2)[wrow]);
+        d = half_of_bits(static_cast<const uint16_t *>(a.s2)[wrow]);
 
     float16_t acc[2];
 #pragma unroll

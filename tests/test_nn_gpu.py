@@ -502,6 +502,30 @@ def test_fused_prefill_experts_of_many_tiles(device, member, n):
     assert np.array_equal(_bits(parts), _bits(fused))
 
 
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+@pytest.mark.parametrize("n", (2048, 4096))
+def test_fused_prefill_weights_are_the_producers(device, member, n):
+    """A one-hot activation row e_k makes a fused output the weight column k
+    itself: one product w * 1 and zeros, exact in f32 and again in fp16.  So
+    every decoded weight the fused GEMM forms in registers is checked against
+    the producer's dequantized stack by value (a -0 weight comes out +0 after
+    the zero products, so zeros compare by value)."""
+    print(f"fused weights {member} n={n}", flush=True)
+    module, _ = _module(member, n, wirepack.seed_for(member, n, "onehot"), device)
+    stack = module.dequantized().float().cpu().numpy()  # [E, OUT, n]
+    rng = np.random.default_rng(149)
+    per_expert = 40  # two 32-slot blocks: both MFMA row blocks carry columns
+    cols = np.stack([rng.choice(n, per_expert, replace=False) for _ in range(EXPERTS)])
+    idx = np.repeat(np.arange(EXPERTS), per_expert).astype(np.int32).reshape(-1, 1)
+    x = np.zeros((idx.shape[0], 1, 1, n), dtype=np.float16)
+    x[np.arange(idx.shape[0]), 0, 0, cols.reshape(-1)] = 1.0
+    module.fused_prefill = True
+    got = module(torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device), sorted_indices=True)
+    got = got.float().cpu().numpy().reshape(EXPERTS, per_expert, OUT)
+    want = np.stack([stack[e][:, cols[e]].T for e in range(EXPERTS)])
+    assert np.array_equal(got, want)
+
+
 @pytest.mark.parametrize("member", ("iq2_ks", "iq1_s_r4"))
 def test_fused_prefill_at_the_routed_geometry(device, member):
     """256 experts at the gate/up geometry, a Zipf-skewed 64-token top-6
