@@ -186,7 +186,9 @@ void fused_gemm_kernel(FusedArgs a) {
     // Offsets and row indices are device data: a slot outside [0, n_slots)
     // is never stored, a row outside x is never read (its output row is 0),
     // and a weight row past out_features is never stored.  Loads of such
-    // rows read an in-bounds row instead, so the step has no branches.
+    // rows read an in-bounds row instead, so the step has no branches but
+    // (IQ1_S_R4) the one that skips staging activation rows past the tile's
+    // end.
     const uint32_t gend = min(a.offs[g + 1], a.n_slots);
     const uint32_t m0 = a.offs[g] + mtile * kFusedBM;
     const uint32_t n0 = cblock * kFusedBN;
@@ -216,13 +218,23 @@ void fused_gemm_kernel(FusedArgs a) {
     const uint32_t xrow = xp < gend ? a.xr[xp] : a.n_x_rows;
     const bool xv = xrow < a.n_x_rows;
     const uint8_t *xsrc = reinterpret_cast<const uint8_t *>(a.x) + size_t(xv ? xrow : 0u) * K * 2 + kXBytes * xseg;
+    // A row past the tile's last slot feeds only MFMA rows that are never
+    // stored, so IQ1_S_R4 neither loads nor stages it (its LDS row keeps
+    // whatever it held): a partial tile (most tiles of a skewed routing)
+    // stages only its slots, and the boundary is uniform per wavefront but
+    // for one.  Measured on the 2048-token Zipf prefill: IQ1_S_R4 -4%; the
+    // IQ2 members, whose step the branch splits for the scheduler, +1 to +2%,
+    // so they stage every row.
+    const bool xlive = !IQ1 || xp < gend;
     const auto load_x = [&](int s, uint4_t *v) {
+        if (!xlive) return;
 #pragma unroll
         for (int i = 0; i < kXBytes / 16; ++i) v[i] = load_u4(xsrc + 2 * kFusedKS * s + 16 * i);
     };
     // Each 8-element chunk is stored in the order (0,4,1,5,2,6,3,7), the
     // order expand_word_paired gives the weights.
     const auto store_x = [&](int buf, const uint4_t *v) {
+        if (!xlive) return;
         uint8_t *dst = xs[buf] + xrow_l * kXStride + kXBytes * xseg;
 #pragma unroll
         for (int i = 0; i < kXBytes / 16; ++i)
