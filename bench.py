@@ -21,7 +21,9 @@ Protocol (reference: bench/price.py): validation before timing; decode and
 floor arms alternated with the order reversed each round; each arm is a
 captured graph of back-to-back dispatches whose routing variants are disjoint
 chunks of expert permutations, so an expert's bytes are re-read only after
-more than 1 GB of other traffic (beyond the 256 MB MALL).
+more than 1 GB of other traffic (beyond the 256 MB MALL).  The prefill cell
+times each of its kernels over four back-to-back dispatches, three rounds
+alternating the routes.
 """
 
 from __future__ import annotations
@@ -339,23 +341,27 @@ def prefill_cell(torch, device, args, seed: int):
         offs_e = torch.zeros(EXPERTS + 1, dtype=torch.int32, device=device)
         offs_e[1:] = torch.from_numpy(np.cumsum(counts).astype(np.int32)).to(device)
         yf = torch.empty((flat.size, out), dtype=torch.float16, device=device)
-        reps = 3
+        yg = torch.empty((rows.numel(), out), dtype=torch.float16, device=device)
+        # each kernel timed over `burst` back-to-back dispatches (steady state, as
+        # a prefill's projections run), rounds alternating the routes
+        reps, burst = 3, 4
         times = {"producer": [], "floor": [], "gemm": [], "fused": []}
         for _ in range(reps):
             for key in ("producer", "floor", "gemm", "fused"):
                 a, b = ev(), ev()
                 a.record()
-                if key == "gemm":
-                    kernels.grouped_gemm(xin.reshape(-1, n), w, offs, rows)
-                elif key == "fused":
-                    kernels.fused_matmul(member, xin.reshape(-1, n), mod._streams(), EXPERTS, out, offs_e, rows,
-                                         out=yf)
-                else:
-                    kernels.dequant(member, mod._streams(), EXPERTS, out, n, slot_of_expert=slot, n_slots=n_slots,
-                                    out=w, floor=(key == "floor"))
+                for _ in range(burst):
+                    if key == "gemm":
+                        kernels.grouped_gemm(xin.reshape(-1, n), w, offs, rows, out=yg)
+                    elif key == "fused":
+                        kernels.fused_matmul(member, xin.reshape(-1, n), mod._streams(), EXPERTS, out, offs_e, rows,
+                                             out=yf)
+                    else:
+                        kernels.dequant(member, mod._streams(), EXPERTS, out, n, slot_of_expert=slot,
+                                        n_slots=n_slots, out=w, floor=(key == "floor"))
                 b.record()
                 b.synchronize()
-                times[key].append(a.elapsed_time(b) * 1e3)
+                times[key].append(a.elapsed_time(b) * 1e3 / burst)
         med = {k: statistics.median(v) for k, v in times.items()}
         kernels.dequant(member, mod._streams(), EXPERTS, out, n, slot_of_expert=slot, n_slots=n_slots, out=w)
         yp = kernels.grouped_gemm(xin.reshape(-1, n), w, offs, rows).float()  # the producer route's output
