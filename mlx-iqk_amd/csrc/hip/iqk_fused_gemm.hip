@@ -97,16 +97,18 @@ struct FusedScales {
     uint8_t dv[kFusedBN * DV_S];
 };
 
-// Copy `rows` rows of a plane (bytes_per_row each, consecutive in global
-// memory) into LDS rows of `stride` bytes, in 16-bit units (every plane's row
-// is a whole number of them).
-__device__ __forceinline__ void copy_plane(const uint8_t *src, int rows, int bytes_per_row, uint8_t *dst, int stride,
-                                           int tid) {
-    const int units_per_row = bytes_per_row / 2;
-    const int units = rows * units_per_row;
+// Copy `rows` rows of a plane (BYTES a row, consecutive in global memory)
+// into LDS rows of STRIDE bytes, in 32-bit units where the rows are whole
+// dwords (every plane but IQ2_KS's per-row scale), else 16-bit units.
+template <int BYTES, int STRIDE>
+__device__ __forceinline__ void copy_plane(const uint8_t *src, int rows, uint8_t *dst, int tid) {
+    using Unit = std::conditional_t<BYTES % 4 == 0, uint32_t, uint16_t>;
+    static_assert(BYTES % sizeof(Unit) == 0 && STRIDE % sizeof(Unit) == 0, "whole units a row");
+    constexpr int UNITS_PER_ROW = BYTES / sizeof(Unit);
+    const int units = rows * UNITS_PER_ROW;
     for (int u = tid; u < units; u += kFusedThreads) {
-        const int r = u / units_per_row, c = u - r * units_per_row;
-        *reinterpret_cast<uint16_t *>(dst + r * stride + 2 * c) = reinterpret_cast<const uint16_t *>(src)[u];
+        const int r = u / UNITS_PER_ROW, c = u - r * UNITS_PER_ROW;
+        *reinterpret_cast<Unit *>(dst + r * STRIDE + sizeof(Unit) * c) = reinterpret_cast<const Unit *>(src)[u];
     }
 }
 
@@ -201,15 +203,15 @@ void fused_gemm_kernel(FusedArgs a) {
         if (tid < IQK_IQ1S_GRID_SIZE * 2 / 16)
             reinterpret_cast<uint4_t *>(sc.codes)[tid] = reinterpret_cast<const uint4_t *>(iqk_iq1s_grid_codes)[tid];
     } else {
-        copy_plane(static_cast<const uint8_t *>(a.s1) + row0 * S::SCL, rows_here, S::SCL, sc.scl, S::SCL_S, tid);
+        copy_plane<S::SCL, S::SCL_S>(static_cast<const uint8_t *>(a.s1) + row0 * S::SCL, rows_here, sc.scl, tid);
     }
     if constexpr (MEMBER == IQ2_KS) {
-        copy_plane(static_cast<const uint8_t *>(a.s2) + row0 * S::HB, rows_here, S::HB, sc.hb, S::HB_S, tid);
-        copy_plane(static_cast<const uint8_t *>(a.s3) + row0 * S::EX, rows_here, S::EX, sc.ex, S::EX_S, tid);
-        copy_plane(static_cast<const uint8_t *>(a.s4) + row0 * S::DV, rows_here, S::DV, sc.dv, S::DV_S, tid);
+        copy_plane<S::HB, S::HB_S>(static_cast<const uint8_t *>(a.s2) + row0 * S::HB, rows_here, sc.hb, tid);
+        copy_plane<S::EX, S::EX_S>(static_cast<const uint8_t *>(a.s3) + row0 * S::EX, rows_here, sc.ex, tid);
+        copy_plane<S::DV, S::DV_S>(static_cast<const uint8_t *>(a.s4) + row0 * S::DV, rows_here, sc.dv, tid);
     } else if constexpr (MEMBER == IQ2_K) {
-        copy_plane(static_cast<const uint8_t *>(a.s2) + row0 * S::EX, rows_here, S::EX, sc.ex, S::EX_S, tid);
-        copy_plane(static_cast<const uint8_t *>(a.s3) + row0 * S::DV, rows_here, S::DV, sc.dv, S::DV_S, tid);
+        copy_plane<S::EX, S::EX_S>(static_cast<const uint8_t *>(a.s2) + row0 * S::EX, rows_here, sc.ex, tid);
+        copy_plane<S::DV, S::DV_S>(static_cast<const uint8_t *>(a.s3) + row0 * S::DV, rows_here, sc.dv, tid);
     }
 
     // activation staging: thread t moves kXBytes of slot row t / kXSegs per step
