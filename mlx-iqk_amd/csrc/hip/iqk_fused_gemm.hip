@@ -176,6 +176,10 @@ void fused_gemm_kernel(FusedArgs a) {
     constexpr int STEPS = K / kFusedKS;
     __shared__ TileScan ts;
     __shared__ __attribute__((aligned(16))) uint8_t xs[2][kFusedBM * kXStride];
+    // per slot of the tile: its output row, bit 31 set when its activations
+    // are real (else its output row is 0), or kNoStore
+    __shared__ uint32_t slot_dst[kFusedBM];
+    constexpr uint32_t kNoStore = 0x7fffffffu;  // above any row (n_slots <= 2^30)
     __shared__ __attribute__((aligned(16))) std::conditional_t<IQ1, FusedGrid, S> sc;
 
     const int tid = threadIdx.x;
@@ -228,6 +232,14 @@ void fused_gemm_kernel(FusedArgs a) {
     // IQ2 members, whose step the branch splits for the scheduler, +1 to +2%,
     // so they stage every row.
     const bool xlive = !IQ1 || xp < gend;
+    if (xseg == 0) {  // one thread a slot: the epilogue's destination, read once
+        uint32_t dst = kNoStore;
+        if (xp < gend) {
+            const uint32_t yrow = a.yr ? a.yr[xp] : xp;
+            if (yrow < a.n_slots) dst = yrow | (xv ? 0x80000000u : 0u);
+        }
+        slot_dst[xrow_l] = dst;
+    }
     const auto load_x = [&](int s, uint4_t *v) {
         if (!xlive) return;
 #pragma unroll
@@ -350,13 +362,10 @@ void fused_gemm_kernel(FusedArgs a) {
     for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const uint32_t p = m0 + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
-            if (p < gend) {
-                const uint32_t yrow = a.yr ? a.yr[p] : p;
-                const bool live = a.xr[p] < a.n_x_rows;  // its activations were real
-                if (yrow < a.n_slots)
-                    a.y[size_t(yrow) * a.N + n0 + lrow] = live ? uint16_t(float_to_half_bits(acc[mb][r])) : uint16_t(0);
-            }
+            const uint32_t dst = slot_dst[32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3)];
+            if (dst != kNoStore)
+                a.y[size_t(dst & 0x7fffffffu) * a.N + n0 + lrow] =
+                    (dst >> 31) ? uint16_t(float_to_half_bits(acc[mb][r])) : uint16_t(0);
         }
     }
 }
