@@ -64,8 +64,8 @@ __device__ __forceinline__ int lane_id() { return int(__lane_id()); }
 
 // Shared memory of the grouped work-list scan.
 struct TileScan {
-    uint32_t scan[256];
-    uint32_t group, mtile, total;
+    uint32_t scan[4];  // the scanning wavefronts' totals
+    uint32_t group, mtile;
 };
 
 // The (group, M-tile) of work item t for a block of THREADS >= 256 threads
@@ -78,7 +78,7 @@ template <int BM, int THREADS = 256>
 __device__ __forceinline__ bool find_mtile(const uint32_t *offs, uint32_t n_groups, uint32_t t, TileScan &ts,
                                            uint32_t &group, uint32_t &mtile) {
     static_assert(THREADS >= 256, "the first 256 threads scan");
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid == 0) ts.group = 0xffffffffu;
     uint32_t carry = 0;
     for (uint32_t base = 0; base < n_groups; base += 256) {
@@ -88,24 +88,26 @@ __device__ __forceinline__ bool find_mtile(const uint32_t *offs, uint32_t n_grou
             const uint32_t c = offs[g + 1] - offs[g];
             cnt = (c + BM - 1) / BM;
         }
-        __syncthreads();
-        if (tid < 256) ts.scan[tid] = cnt;
-        __syncthreads();
-        for (int off = 1; off < 256; off <<= 1) {
-            const uint32_t v = tid >= off && tid < 256 ? ts.scan[tid - off] : 0u;
-            __syncthreads();
-            if (tid < 256) ts.scan[tid] += v;
-            __syncthreads();
+        // inclusive prefix within the wavefront, then the four wavefront
+        // totals through LDS
+        uint32_t incl = cnt;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t up = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += up;
         }
-        const uint32_t incl = carry + (tid < 256 ? ts.scan[tid] : 0u);
+        if (tid < 256 && lane == 63) ts.scan[wave] = incl;
+        __syncthreads();  // also orders tid 0's reset of ts.group before any match below
+        uint32_t before = carry;
+        for (int w = 0; w < wave && w < 4; ++w) before += ts.scan[w];
+        incl += before;
         const uint32_t excl = incl - cnt;
-        if (cnt && t >= excl && t < incl) {
+        if (tid < 256 && cnt && t >= excl && t < incl) {
             ts.group = g;
             ts.mtile = t - excl;
         }
-        if (tid == 255) ts.total = incl;
-        __syncthreads();
-        carry = ts.total;
+        carry += ts.scan[0] + ts.scan[1] + ts.scan[2] + ts.scan[3];
+        __syncthreads();  // the next round rewrites the totals
     }
     __syncthreads();
     group = ts.group;
