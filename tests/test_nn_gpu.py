@@ -504,14 +504,20 @@ def test_fused_prefill_experts_of_many_tiles(device, member, n):
 
 @pytest.mark.parametrize("member", fmt.MEMBERS)
 @pytest.mark.parametrize("n", (2048, 4096))
-def test_fused_prefill_weights_are_the_producers(device, member, n):
+@pytest.mark.parametrize("scales", ("serving", "tiny"))
+def test_fused_prefill_weights_are_the_producers(device, member, n, scales):
     """A one-hot activation row e_k makes a fused output the weight column k
     itself: one product w * 1 and zeros, exact in f32 and again in fp16.  So
     every decoded weight the fused GEMM forms in registers is checked against
     the producer's dequantized stack by value (a -0 weight comes out +0 after
-    the zero products, so zeros compare by value)."""
-    print(f"fused weights {member} n={n}", flush=True)
-    module, _ = _module(member, n, wirepack.seed_for(member, n, "onehot"), device)
+    the zero products, so zeros compare by value).  `tiny` scales are all
+    subnormal, so many table entries are subnormal or round to zero: the fp16
+    table arithmetic must round them as the producer's f32 chain does."""
+    print(f"fused weights {member} n={n} {scales}", flush=True)
+    wire = wirepack.random_wire(member, EXPERTS * OUT, n, seed=wirepack.seed_for(member, n, "onehot"), scales=scales)
+    shapes = fmt.component_shapes(member, EXPERTS, OUT, n)
+    module = IqkSwitchLinear(member, EXPERTS, OUT, n, device=device)
+    module.load_streams({k: np.ascontiguousarray(v).reshape(shapes[k]) for k, v in fmt.pack(member, wire, n).items()})
     stack = module.dequantized().float().cpu().numpy()  # [E, OUT, n]
     rng = np.random.default_rng(149)
     per_expert = 40  # two 32-slot blocks: both MFMA row blocks carry columns
@@ -523,6 +529,9 @@ def test_fused_prefill_weights_are_the_producers(device, member, n):
     got = module(torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device), sorted_indices=True)
     got = got.float().cpu().numpy().reshape(EXPERTS, per_expert, OUT)
     want = np.stack([stack[e][:, cols[e]].T for e in range(EXPERTS)])
+    assert np.isfinite(want).all()
+    if scales == "tiny":  # the case is what it says: many subnormal weights
+        assert np.mean((want != 0) & (np.abs(want) < 2.0 ** -14)) > 0.1
     assert np.array_equal(got, want)
 
 

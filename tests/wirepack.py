@@ -38,11 +38,22 @@ def serving_half(rng: np.random.Generator, size) -> np.ndarray:
     return (mag * np.where(rng.random(size) < 0.5, -1.0, 1.0)).astype(np.float16)
 
 
+def tiny_half(rng: np.random.Generator, size) -> np.ndarray:
+    """Subnormal fp16 scales (either sign), mantissas log-uniform so many are a
+    few ulps of 2^-24: a large share of decoded weights come out subnormal (or
+    round to zero), and none overflows."""
+    e = rng.integers(0, 10, size=size)
+    bits = rng.integers(1 << e, 1 << (e + 1), dtype=np.int64) | np.where(rng.random(size) < 0.5, 0x8000, 0)
+    return bits.astype(np.uint16).view(np.float16)
+
+
 def _scales(rng, size, mode):
     if mode == "sweep":
         return finite_half(rng, size)
     if mode == "serving":
         return serving_half(rng, size)
+    if mode == "tiny":
+        return tiny_half(rng, size)
     raise ValueError(mode)
 
 
@@ -152,7 +163,7 @@ def exhaustive_iq1_s_r4(seed: int = 0) -> np.ndarray:
 def random_wire(member: str, rows: int, n: int, seed: int, scales: str = "sweep") -> np.ndarray:
     """Uniformly random wire rows; every field of every member is legal over its
     whole byte space, only the fp16 scales are drawn (``sweep`` = all finite fp16,
-    ``serving`` = converted-row magnitudes)."""
+    ``serving`` = converted-row magnitudes, ``tiny`` = subnormal fp16)."""
     rng = np.random.default_rng(seed)
     if member == "iq1_s_r4":
         assert rows % 4 == 0
