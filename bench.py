@@ -298,7 +298,8 @@ def dequant_cell(torch, device, member: str, args, seed: int):
 
 def prefill_cell(torch, device, args, seed: int):
     """2048 tokens, Zipf(1.1) top-6 sorted routing; gate/up IQ2_KS, down IQ2_K (the
-    totals), and the gate projection once more as IQ1_S_R4 (reported beside them)."""
+    totals), and the gate projection once more as IQ1_S_R4 and as IQ2_K (reported
+    beside them)."""
     from mlx_iqk_amd import format as fmt
     from mlx_iqk_amd import kernels, synth
     from mlx_iqk_amd.nn import IqkSwitchLinear
@@ -313,7 +314,7 @@ def prefill_cell(torch, device, args, seed: int):
     h = torch.randn(flat.size, 1, DN[1], device=device).to(torch.float16)
     ids = torch.from_numpy(flat.astype(np.int32)).to(device)
     projections = (("gate", "iq2_ks", GU, x), ("up", "iq2_ks", GU, x), ("down", "iq2_k", DN, h),
-                   ("gate_iq1_s_r4", "iq1_s_r4", GU, x))
+                   ("gate_iq1_s_r4", "iq1_s_r4", GU, x), ("gate_iq2_k", "iq2_k", GU, x))
     res = {"tokens": tokens, "pairs": int(flat.size), "experts_routed": int((counts > 0).sum()),
            "max_pairs_per_expert": int(counts.max()), "projections": {}}
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
@@ -386,7 +387,7 @@ def prefill_cell(torch, device, args, seed: int):
             f"  fused {med['fused']:.1f} us ({r['fused_tflops']} TFLOP/s, dev {fused_dev:.2e})")
         del mod, w, y, yf, yp
         torch.cuda.empty_cache()
-        if member == "iq1_s_r4":  # outside the prefill configuration's totals
+        if name.startswith("gate_"):  # outside the prefill configuration's totals
             continue
         tot_fused += med["fused"]
         tot_prod += med["producer"]

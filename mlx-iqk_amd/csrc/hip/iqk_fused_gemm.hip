@@ -82,9 +82,14 @@ struct FusedArgs {
 // A block's scale planes in LDS.  IQ2_KS: scl u8 [K/64], sch u8 [K/256],
 // sex u8 [K/256], dv f16 per row.  IQ2_K: scl u16 [K/64], sex u8 [K/128],
 // dv f16 [K/256].  Row strides are padded to an odd number of dwords.
+// IQ2_K at K = 4096 keeps its dv plane out of LDS (DV_IN_LDS false): with it
+// the planes (52 KB for 256 rows) and the activations would fit one block a
+// CU; without it (43 KB), two.  Its lanes load their super-block scales
+// instead, one 32-bit word (two super-blocks) every four steps.
 template <int MEMBER, int K>
 struct FusedScales {
     static constexpr bool KS = MEMBER == IQ2_KS;
+    static constexpr bool DV_IN_LDS = !(MEMBER == IQ2_K && K == 4096);
     static constexpr int SCL = KS ? K / 64 : K / 32;    // bytes per row
     static constexpr int HB = KS ? K / 256 : 0;
     static constexpr int EX = KS ? K / 256 : K / 128;
@@ -94,7 +99,7 @@ struct FusedScales {
     uint8_t scl[kFusedBN * SCL_S];
     uint8_t hb[KS ? kFusedBN * HB_S : 4];
     uint8_t ex[kFusedBN * EX_S];
-    uint8_t dv[kFusedBN * DV_S];
+    uint8_t dv[DV_IN_LDS ? kFusedBN * DV_S : 4];
 };
 
 // Copy `rows` rows of a plane (BYTES a row, consecutive in global memory)
@@ -115,9 +120,12 @@ __device__ __forceinline__ void copy_plane(const uint8_t *src, int rows, uint8_t
 // The v_perm tables of lane (row, kg) at step s, one per 16-weight word of
 // its 64 weights: IQ2_KS sub-blocks 4s + 2kg + h (two words each), IQ2_K
 // sub-blocks 8s + 4kg + w (one word each).  Same f32 chain as the producer.
+// IQ2_K's super-block scale comes from the dv plane, or (no dv plane in
+// LDS) from dvw, the lane's dv word of steps 4(s/4) .. +3 (scales of
+// super-blocks 2(s/4) and 2(s/4)+1).
 template <int MEMBER, int K>
 __device__ __forceinline__ void fused_pools(const FusedScales<MEMBER, K> &sc, int row, int s, int kg, _Float16 d,
-                                            Pool *p) {
+                                            uint32_t dvw, Pool *p) {
     using S = FusedScales<MEMBER, K>;
     if constexpr (MEMBER == IQ2_KS) {
         const uint32_t scl = sc.scl[row * S::SCL_S + 2 * s + kg];  // nibbles of sub-blocks 4s+2kg, +1
@@ -134,7 +142,11 @@ __device__ __forceinline__ void fused_pools(const FusedScales<MEMBER, K> &sc, in
     } else {
         const uint32_t scw = *reinterpret_cast<const uint16_t *>(sc.scl + row * S::SCL_S + 2 * (2 * s + kg));
         const uint32_t ab = sc.ex[row * S::EX_S + s] >> (4 * kg);
-        const _Float16 dd = half_of_bits(*reinterpret_cast<const uint16_t *>(sc.dv + row * S::DV_S + 2 * (s >> 1)));
+        _Float16 dd;
+        if constexpr (S::DV_IN_LDS)
+            dd = half_of_bits(*reinterpret_cast<const uint16_t *>(sc.dv + row * S::DV_S + 2 * (s >> 1)));
+        else
+            dd = half_of_bits(dvw >> (16 * ((s >> 1) & 1)));
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
             const int idx = int((scw >> (4 * w)) & 15u) - 8;
@@ -215,7 +227,8 @@ void fused_gemm_kernel(FusedArgs a) {
         copy_plane<S::DV, S::DV_S>(static_cast<const uint8_t *>(a.s4) + row0 * S::DV, rows_here, sc.dv, tid);
     } else if constexpr (MEMBER == IQ2_K) {
         copy_plane<S::EX, S::EX_S>(static_cast<const uint8_t *>(a.s2) + row0 * S::EX, rows_here, sc.ex, tid);
-        copy_plane<S::DV, S::DV_S>(static_cast<const uint8_t *>(a.s3) + row0 * S::DV, rows_here, sc.dv, tid);
+        if constexpr (S::DV_IN_LDS)
+            copy_plane<S::DV, S::DV_S>(static_cast<const uint8_t *>(a.s3) + row0 * S::DV, rows_here, sc.dv, tid);
     }
 
     // activation staging: thread t moves kXBytes of slot row t / kXSegs per step
@@ -277,6 +290,10 @@ void fused_gemm_kernel(FusedArgs a) {
 
     uint4_t xa[kXBytes / 16];
     load_x(0, xa);
+    // IQ2_K without a dv plane in LDS: this lane's dv words, one per four steps
+    const uint32_t *dvp = reinterpret_cast<const uint32_t *>(static_cast<const uint8_t *>(a.s3) + wrow * (K / 128));
+    constexpr bool DV_WORDS = MEMBER == IQ2_K && !S::DV_IN_LDS;
+    uint32_t dvw = DV_WORDS ? dvp[0] : 0u, dvn = 0u;
     uint4_t q = load_q(0), qn;
     store_x(0, xa);
     __syncthreads();  // scale planes and the first activations are in LDS
@@ -305,12 +322,15 @@ void fused_gemm_kernel(FusedArgs a) {
                 load_x(s + 1, xa);
                 qn = load_q(s + 1);
             }
+            if constexpr (DV_WORDS) {
+                if ((s & 3) == 0 && s + 4 < STEPS) dvn = dvp[(s >> 2) + 1];  // the next group's word, a group ahead
+            }
             Pool p[4];
             uint32_t words[4];
             if constexpr (IQ1) {
                 fused_iq1(q, sc.codes, d, p, words);
             } else {
-                fused_pools<MEMBER, K>(sc, lrow, s, kg, d, p);
+                fused_pools<MEMBER, K>(sc, lrow, s, kg, d, dvw, p);
 #pragma unroll
                 for (int w = 0; w < 4; ++w) words[w] = q[w];
             }
@@ -346,6 +366,9 @@ void fused_gemm_kernel(FusedArgs a) {
             if (more) {
                 store_x((s + 1) & 1, xa);  // the buffer every wavefront finished reading before the last barrier
                 q = qn;
+            }
+            if constexpr (DV_WORDS) {
+                if ((s & 3) == 3) dvw = dvn;
             }
             __syncthreads();
         }
