@@ -535,10 +535,11 @@ def test_fused_prefill_weights_are_the_producers(device, member, n, scales):
     assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("member", ("iq2_ks", "iq1_s_r4"))
+@pytest.mark.parametrize("member", fmt.MEMBERS)
 def test_fused_prefill_at_the_routed_geometry(device, member):
     """256 experts at the gate/up geometry, a Zipf-skewed 64-token top-6
-    prefill: sampled output rows against float64."""
+    prefill: sampled output rows against float64.  IQ2_K at this width is the
+    form whose super-block scales come from global memory, not LDS."""
     print(f"fused prefill routed geometry {member}", flush=True)
     E, out, n = 256, 2048, 4096
     wire = wirepack.random_wire(member, E * out, n, seed=2026, scales="serving")
