@@ -718,8 +718,8 @@ enum GemvMode : int {
 
 // R = 1: six wavefronts per SIMD, three workgroups of eight (N = 4096) or
 // six of four (N = 2048) per CU, so a 1-token routed decode's 768
-// workgroups are resident at once.  R = 2 (IQ1_S_R4 dispatches of many
-// workgroups): each wavefront takes 32 rows, two MFMA column blocks that
+// workgroups are resident at once.  R = 2 (dispatches of many workgroups:
+// IQ1_S_R4, and the IQ2 members at 2048 wide): each wavefront takes 32 rows, two MFMA column blocks that
 // share every A read, so a workgroup stages its activations for 64 rows;
 // five wavefronts per SIMD.  kUnion re-expands a lane's stream words for
 // each pair of its run (the words are read once); five wavefronts per SIMD.
@@ -906,11 +906,14 @@ int launch_member(int member, int64_t n, const Gemv2Args &a, uint32_t mats, hipS
     }
 }
 
-// IQ1_S_R4 dispatches of at least this many 32-row workgroups (four times
-// the 768 of a 1-token decode) take two row blocks per wavefront.  The IQ2
-// members measured slower that way at 4 tokens and no faster at 8: they keep
-// one block.
+// Dispatches of many 32-row workgroups take two row blocks per wavefront:
+// IQ1_S_R4 at either width from four times the 768 of a 1-token decode, the
+// IQ2 members at 2048 wide (the down projection) from eight times (top-6 down
+// measured 2-4% slower with two blocks at 4 tokens, 2-4% faster at 8 and 6-7%
+// at 32).  The IQ2 members' 4096-wide dispatches keep one block (1-2% slower
+// with two).
 constexpr uint64_t kTwoRowMinGroups = 4 * 768;
+constexpr uint64_t kTwoRowMinGroupsIq2 = 8 * 768;
 
 // Called by the GEMV entry points (after their argument checks) when
 // out_features is a multiple of the workgroup's 32 rows; returns -1 when this
@@ -941,11 +944,13 @@ int gemv_mfma_dispatch(bool floor, int member, int64_t n, int64_t out, int64_t n
     a.out_features = uint32_t(out);
     a.y = static_cast<uint16_t *>(y);
     if (!toks) {
-        const bool two = member == IQK_MEMBER_IQ1_S_R4 && out % (2 * kGroupRows) == 0 &&
-                         uint64_t(mats) * uint64_t(out / kGroupRows) >= kTwoRowMinGroups;
+        const uint64_t groups = uint64_t(mats) * uint64_t(out / kGroupRows);
+        const bool two = out % (2 * kGroupRows) == 0 &&
+                         (member == IQK_MEMBER_IQ1_S_R4 ? groups >= kTwoRowMinGroups
+                                                        : n == 2048 && groups >= kTwoRowMinGroupsIq2);
         if (two)
-            return floor ? launch_gemv_mfma<IQ1_S_R4, true, kPairs, 2>(n, a, mats, st)
-                         : launch_gemv_mfma<IQ1_S_R4, false, kPairs, 2>(n, a, mats, st);
+            return floor ? launch_member<true, kPairs, 2>(member, n, a, mats, st)
+                         : launch_member<false, kPairs, 2>(member, n, a, mats, st);
         return floor ? launch_member<true, kPairs, 1>(member, n, a, mats, st)
                      : launch_member<false, kPairs, 1>(member, n, a, mats, st);
     }

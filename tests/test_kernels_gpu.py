@@ -142,13 +142,14 @@ def test_gemv_matches_a_float64_reference_per_pair_rows(device, member, n):
 @pytest.mark.parametrize("member", fmt.MEMBERS)
 @pytest.mark.parametrize("n", kernels.SUPPORTED_IN_FEATURES)
 def test_gemv_large_dispatch_equals_small_dispatches(device, member, n):
-    """An IQ1_S_R4 dispatch of >= 4 x 768 row workgroups takes two 16-row
-    blocks per wavefront (shared activation reads); a row's arithmetic is the
-    same, so its outputs equal those of the same pairs in small one-block
-    dispatches bit for bit, and meet the float64 gate.  The IQ2 members (one
+    """A large dispatch takes two 16-row blocks per wavefront (shared
+    activation reads): IQ1_S_R4 from 4 x 768 row workgroups, the IQ2 members at
+    2048 wide from 8 x 768.  A row's arithmetic is the same, so its outputs
+    equal those of the same pairs in small one-block dispatches bit for bit,
+    and meet the float64 gate.  The IQ2 members' 4096-wide dispatches (one
     block at any size) and their sorted form are held to the same."""
     print(f"gemv large dispatch {member} n={n}", flush=True)
-    out, tokens, top_k = 256, 128, 3  # 384 pairs x 8 row workgroups = 3072
+    out, tokens, top_k = 256, 256, 3  # 768 pairs x 8 row workgroups = 6144
     _, streams, ref = _case(member, n, wirepack.seed_for(member, n, "large"), device, out=out)
     rng = np.random.default_rng(23)
     x = rng.standard_normal((tokens, n)).astype(np.float16)
