@@ -907,12 +907,13 @@ int launch_member(int member, int64_t n, const Gemv2Args &a, uint32_t mats, hipS
 }
 
 // Dispatches of many 32-row workgroups take two row blocks per wavefront:
-// IQ1_S_R4 at either width from four times the 768 of a 1-token decode, the
-// IQ2 members at 2048 wide (the down projection) from eight times (top-6 down
-// measured 2-4% slower with two blocks at 4 tokens, 2-4% faster at 8 and 6-7%
-// at 32).  The IQ2 members' 4096-wide dispatches keep one block (1-2% slower
-// with two).
-constexpr uint64_t kTwoRowMinGroups = 4 * 768;
+// IQ1_S_R4 at either width from twice the 768 of a 1-token decode (top-6
+// measured 5-10% faster with two blocks at 2 and 3 tokens, 13% slower at 1),
+// the IQ2 members at 2048 wide (the down projection) from eight times (top-6
+// down measured 2-4% slower with two blocks at 4 tokens, 2-4% faster at 8 and
+// 6-7% at 32).  The IQ2 members' 4096-wide dispatches keep one block (1-2%
+// slower with two).
+constexpr uint64_t kTwoRowMinGroups = 2 * 768;
 constexpr uint64_t kTwoRowMinGroupsIq2 = 8 * 768;
 
 // Called by the GEMV entry points (after their argument checks) when

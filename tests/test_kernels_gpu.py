@@ -143,7 +143,7 @@ def test_gemv_matches_a_float64_reference_per_pair_rows(device, member, n):
 @pytest.mark.parametrize("n", kernels.SUPPORTED_IN_FEATURES)
 def test_gemv_large_dispatch_equals_small_dispatches(device, member, n):
     """A large dispatch takes two 16-row blocks per wavefront (shared
-    activation reads): IQ1_S_R4 from 4 x 768 row workgroups, the IQ2 members at
+    activation reads): IQ1_S_R4 from 2 x 768 row workgroups, the IQ2 members at
     2048 wide from 8 x 768.  A row's arithmetic is the same, so its outputs
     equal those of the same pairs in small one-block dispatches bit for bit,
     and meet the float64 gate.  The IQ2 members' 4096-wide dispatches (one
