@@ -9,7 +9,9 @@ convention (bench/price.py:146).  Inputs are resident in HBM; the K timed
 steps replay as one captured HIP graph between two synchronisations.
 
 Also reported, outside the timed region: every member's decode against its
-own deleted-decode floor (IQ2_KS and IQ1_S_R4 at 1 token, IQ2_K at 8 tokens),
+own deleted-decode floor (IQ2_KS and IQ1_S_R4 at 1 token, IQ2_K at 8 tokens)
+and against a pure byte stream of the same size (IQ1_S_R4 also against the
+floor that keeps its grid lookups, the reference's IQ1 floor),
 the dequant producer against its floor and its row-range form, the Zipf(1.1)
 mixed-member prefill (producer GB/s, grouped-GEMM and fused-GEMM TFLOP/s and
 MFMA utilisation), the sorted and union decode forms on uniform multi-token
@@ -21,9 +23,18 @@ Protocol (reference: bench/price.py): validation before timing; decode and
 floor arms alternated with the order reversed each round; each arm is a
 captured graph of back-to-back dispatches whose routing variants are disjoint
 chunks of expert permutations, so an expert's bytes are re-read only after
-more than 1 GB of other traffic (beyond the 256 MB MALL).  The prefill cell
-times each of its kernels over four back-to-back dispatches, three rounds
-alternating the routes.
+more than 1 GB of other traffic (beyond the 256 MB MALL).  The stream arm
+reads the same byte count per dispatch from windows that walk a 2 GiB buffer.
+The prefill cell times each of its kernels over four back-to-back dispatches,
+three rounds alternating the routes.
+
+Gates per cell, as the reference's (bench/price.py:458-470): the floor
+streams inside the band [2000, 8000] GB/s (a quarter of HBM peak up to the
+peak: a floor above it would read fewer bytes than it claims);
+no_deleted_load_signature -- the decode is not faster than its own floor by
+more than the two arms' spread; within_bar -- decode / floor <= 1.15 (the
+producer: <= 1.05).  The JSON line carries every cell's ratios and gates;
+``--json-out`` also writes the full results.
 """
 
 from __future__ import annotations
@@ -46,6 +57,9 @@ for _p in (ROOT / "mlx-iqk_amd", ROOT):
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
+FLOOR_BAND_GBS = (2000.0, HBM_PEAK_GBS)
+DECODE_BAR, PRODUCER_BAR = 1.15, 1.05
+STREAM_BUFFER_BYTES = 2 << 30
 EXPERTS, TOP_K = 256, 6
 PROBE_COPY_BYTES = 64 << 20
 GU = (2048, 4096)   # gate/up: out, in
@@ -64,14 +78,18 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--rounds", type=int, default=5, help="alternated decode/floor rounds per cell")
     ap.add_argument("--block", type=int, default=200, help="dispatches per captured graph in a cell")
     ap.add_argument("--distinct", type=int, default=2, help="distinct quantized experts per projection")
-    ap.add_argument("--cells", default="iq2_ks,iq2_k,iq1_s_r4,dequant,prefill,pack,verify,quantize")
+    ap.add_argument("--cells", default="iq2_ks,iq2_k,iq1_s_r4,dequant,prefill,pack,verify,quantize",
+                    help="cells after the headline ('headline' alone: the IQ2_KS cell and the headline only)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="CPU baseline sample budget (half on one thread, half on every core)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--json-out", default=None)
     ap.add_argument("--probe", type=int, default=0, metavar="K",
-                    help="counter-probe mode: K eager IQ2_KS gate/up decode dispatches, then K copies of "
+                    help="counter-probe mode: K eager dispatches of --probe-kernel, then K copies of "
                          f"{PROBE_COPY_BYTES >> 20} MiB (the HBM-byte calibration), and exit")
+    ap.add_argument("--probe-kernel", default="decode:iq2_ks:1:gate_up",
+                    help="decode|floor|floor_grid:<member>:<tokens>:gate_up|down, or fused|producer|gemm:<member>:"
+                         "gate|down (the 2048-token Zipf prefill)")
     return ap.parse_args()
 
 
@@ -132,8 +150,32 @@ def disjoint_selections(rng, count: int, tokens: int) -> list[np.ndarray]:
 # ---------------------------------------------------------------- decode cells ---
 
 
+class StreamWindows:
+    """The stream arm's source: windows of one dispatch's byte count walking a
+    2 GiB device buffer, so a window is re-read only after > 1 GiB of others."""
+
+    def __init__(self, torch, device):
+        self.buf = torch.zeros(STREAM_BUFFER_BYTES, dtype=torch.uint8, device=device)
+        self.out = torch.empty(STREAM_BUFFER_BYTES // 4096, dtype=torch.int32, device=device)
+
+    def launcher(self, nbytes: int, i: int):
+        from mlx_iqk_amd import kernels
+        span = (nbytes + 4095) // 4096 * 4096
+        slots = max(1, STREAM_BUFFER_BYTES // span)
+        view = self.buf[(i % slots) * span:]
+        return lambda: kernels.stream_floor(view, nbytes, out=self.out)
+
+
+def gate_cell(res: dict, bar: float) -> dict:
+    """The reference's three gates for one cell (bench/price.py:458-470)."""
+    spread = (res["decode"]["max_us"] - res["decode"]["min_us"]) + (res["floor"]["max_us"] - res["floor"]["min_us"])
+    return {"floor_in_band": bool(FLOOR_BAND_GBS[0] <= res["floor"]["gb_per_s"] <= FLOOR_BAND_GBS[1]),
+            "no_deleted_load_signature": bool(res["floor"]["median_us"] - res["decode"]["median_us"] <= spread),
+            "within_bar": bool(res["x_floor"] <= bar)}
+
+
 def decode_cell(torch, device, member: str, tokens: int, args, seed: int, want_steps: bool = False,
-                launchers_only: bool = False):
+                launchers_only: bool = False, windows: StreamWindows | None = None):
     from mlx_iqk_amd import format as fmt
     from mlx_iqk_amd import kernels, synth
 
@@ -158,12 +200,12 @@ def decode_cell(torch, device, member: str, tokens: int, args, seed: int, want_s
             "dn_y": torch.empty(dn_mats, DN[0], dtype=torch.float16, device=device),
         })
 
-    def gu_launch(i, floor=False):
+    def gu_launch(i, floor: bool | str = False):
         v = V[i % variants]
         return lambda: kernels.gemv(member, v["gu_x"], gu, v["gu_sel"], TOP_K, 2 * EXPERTS, GU[0],
                                     floor=floor, out=v["gu_y"])
 
-    def dn_launch(i, floor=False):
+    def dn_launch(i, floor: bool | str = False):
         v = V[i % variants]
         return lambda: kernels.gemv(member, v["dn_x"], dn, v["dn_sel"], 1, EXPERTS, DN[0], floor=floor,
                                     out=v["dn_y"])
@@ -200,16 +242,28 @@ def decode_cell(torch, device, member: str, tokens: int, args, seed: int, want_s
     for name, launch, nbytes in (("gate_up", gu_launch, bytes_gu), ("down", dn_launch, bytes_dn)):
         arms = {"decode": Arm(torch, [launch(i) for i in range(B)], "decode"),
                 "floor": Arm(torch, [launch(i, True) for i in range(B)], "floor")}
+        if windows is not None:
+            arms["stream"] = Arm(torch, [windows.launcher(nbytes, i) for i in range(B)], "stream")
+        if member == "iq1_s_r4":
+            arms["floor_grid"] = Arm(torch, [launch(i, "grid") for i in range(B)], "floor_grid")
         res = alternate(arms, args.rounds)
         res["bytes_per_dispatch"] = nbytes
-        for arm in ("decode", "floor"):
+        for arm in arms:
             res[arm]["gb_per_s"] = round(nbytes / (res[arm]["median_us"] * 1e-6) / 1e9, 1)
             res[arm]["frac_of_8tbps"] = round(res[arm]["gb_per_s"] / HBM_PEAK_GBS, 4)
         res["x_floor"] = round(res["decode"]["median_us"] / res["floor"]["median_us"], 4)
+        if "stream" in arms:
+            res["x_stream"] = round(res["decode"]["median_us"] / res["stream"]["median_us"], 4)
+        if "floor_grid" in arms:
+            res["x_floor_grid"] = round(res["decode"]["median_us"] / res["floor_grid"]["median_us"], 4)
         res["ideal_us_at_8tbps"] = round(nbytes / HBM_PEAK_GBS / 1e3, 3)
+        res["gates"] = gate_cell(res, DECODE_BAR)
         cells[name] = res
         log(f"  {name:8s} decode {res['decode']['median_us']:8.2f} us ({res['decode']['gb_per_s']:7.1f} GB/s)"
-            f"  floor {res['floor']['median_us']:8.2f} us  x{res['x_floor']:.3f}")
+            f"  floor {res['floor']['median_us']:8.2f} us  x{res['x_floor']:.3f}"
+            + (f"  stream {res['stream']['median_us']:.2f} us x{res['x_stream']:.3f}" if "stream" in res else "")
+            + (f"  grid floor {res['floor_grid']['median_us']:.2f} us x{res['x_floor_grid']:.3f}"
+               if "floor_grid" in res else ""))
         del arms
     out = {"member": member, "tokens": tokens, "top_k": TOP_K, "experts": EXPERTS, "validation": validation,
            "cells": cells}
@@ -284,6 +338,7 @@ def dequant_cell(torch, device, member: str, args, seed: int):
         for arm in ("decode", "floor"):
             r[arm]["gb_per_s"] = round((read + written) / (r[arm]["median_us"] * 1e-6) / 1e9, 1)
             r[arm]["frac_of_8tbps"] = round(r[arm]["gb_per_s"] / HBM_PEAK_GBS, 4)
+        r["gates"] = gate_cell(r, PRODUCER_BAR)
         res[name] = r
         log(f"  decode {r['decode']['median_us']:9.2f} us ({r['decode']['gb_per_s']:7.1f} GB/s)  floor "
             f"{r['floor']['median_us']:9.2f} us  x{r['x_floor']:.3f}  half-range {r['range']['median_us']:.2f} us "
@@ -606,23 +661,68 @@ def cpu_baseline(seconds: float, distinct: int, seed: int) -> dict:
             "host_cpus": cores}
 
 
+def prefill_launcher(torch, device, member: str, projection: str, kind: str, args, seed: int = 23):
+    """One kernel of the 2048-token Zipf(1.1) top-6 prefill (sorted pairs), as a
+    launch closure, with its algorithmic bytes and flops per dispatch."""
+    from mlx_iqk_amd import format as fmt
+    from mlx_iqk_amd import kernels, synth
+
+    out, n = GU if projection == "gate" else DN
+    idx = synth.zipf_routing(2048, EXPERTS, TOP_K, 1.1, seed)
+    flat = np.sort(idx.reshape(-1))
+    counts = np.bincount(flat, minlength=EXPERTS)
+    st = synth.expert_stack(member, EXPERTS, out, n, seed, device, args.distinct, f"pf-{projection}")
+    x = torch.randn(flat.size, n, device=device).to(torch.float16)
+    rows = torch.arange(flat.size, dtype=torch.int32, device=device)
+    offs = torch.zeros(EXPERTS + 1, dtype=torch.int32, device=device)
+    offs[1:] = torch.from_numpy(np.cumsum(counts).astype(np.int32)).to(device)
+    y = torch.empty((flat.size, out), dtype=torch.float16, device=device)
+    routed = int((counts > 0).sum())
+    info = {"pairs": int(flat.size), "experts_routed": routed, "flop": 2 * flat.size * out * n,
+            "stream_bytes": routed * out * fmt.ik_row_bytes(member, n)}
+    if kind == "fused":
+        return (lambda: kernels.fused_matmul(member, x, st, EXPERTS, out, offs, rows, out=y)), info
+    slot = torch.arange(EXPERTS, dtype=torch.int32, device=device)
+    w = torch.empty((EXPERTS, out, n), dtype=torch.float16, device=device)
+    kernels.dequant(member, st, EXPERTS, out, n, slot_of_expert=slot, n_slots=EXPERTS, out=w)
+    info["fp16_weight_bytes"] = routed * out * n * 2
+    if kind == "producer":
+        return (lambda: kernels.dequant(member, st, EXPERTS, out, n, slot_of_expert=slot, n_slots=EXPERTS,
+                                        out=w)), info
+    return (lambda: kernels.grouped_gemm(x, w, offs, rows, out=y)), info
+
+
 def probe(torch, device, args) -> int:
-    """Eager dispatches for hardware-counter passes (rocprofv3 --pmc): the
-    headline gate/up decode kernel on its disjoint routing variants, then a
-    plain device copy of known size whose counters calibrate HBM bytes."""
+    """Eager dispatches for hardware-counter passes (rocprofv3 --pmc): K
+    dispatches of one kernel (a decode cell's dispatch on its disjoint routing
+    variants, or one kernel of the Zipf prefill), then a plain device copy of
+    known size whose counters calibrate HBM bytes."""
     from mlx_iqk_amd.format import ik_row_bytes
 
-    gu_launch, _ = decode_cell(torch, device, "iq2_ks", 1, args, seed=11, launchers_only=True)
-    for i in range(args.probe):
-        gu_launch(i)()
+    kind, member, *rest = args.probe_kernel.split(":")
+    info = {"probe": args.probe, "kernel": args.probe_kernel}
+    if kind in ("decode", "floor", "floor_grid"):
+        tokens, which = int(rest[0]), rest[1]
+        gu_launch, dn_launch = decode_cell(torch, device, member, tokens, args, seed=11, launchers_only=True)
+        launch = gu_launch if which == "gate_up" else dn_launch
+        floor = {"decode": False, "floor": True, "floor_grid": "grid"}[kind]
+        out, n = GU if which == "gate_up" else DN
+        mats = (2 if which == "gate_up" else 1) * tokens * TOP_K
+        info["bytes_per_dispatch"] = mats * out * ik_row_bytes(member, n)
+        for i in range(args.probe):
+            launch(i, floor)()
+    else:
+        fn, extra = prefill_launcher(torch, device, member, rest[0], kind, args)
+        info.update(extra)
+        for _ in range(args.probe):
+            fn()
     src = torch.empty(PROBE_COPY_BYTES, dtype=torch.uint8, device=device).random_(0, 255)
     dst = torch.empty_like(src)
     for _ in range(args.probe):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"probe": args.probe, "kernel": "gemv_mfma_kernel<IQ2_KS,4096>",
-                      "bytes_per_dispatch": 2 * TOP_K * GU[0] * ik_row_bytes("iq2_ks", GU[1]),
-                      "copy_bytes": PROBE_COPY_BYTES}), flush=True)
+    info["copy_bytes"] = PROBE_COPY_BYTES
+    print(json.dumps(info), flush=True)
     return 0
 
 
@@ -646,15 +746,20 @@ def main() -> int:
     cells = [c for c in args.cells.split(",") if c]
     results = {}
     t_start = time.time()
+    windows = StreamWindows(torch, device)
     # the headline member always runs: its gate/up kernel is the roofline kernel
-    results["iq2_ks"] = decode_cell(torch, device, "iq2_ks", 1, args, seed=11, want_steps=True)
+    results["iq2_ks"] = decode_cell(torch, device, "iq2_ks", 1, args, seed=11, want_steps=True, windows=windows)
     step = results["iq2_ks"].pop("_step")
     head = headline(torch, step, args.steps, args.warmup)
     log(f"[headline] {args.steps} steps: {head['ms_per_step'] * 1e3:.2f} us/step, {head['gb_per_s']:.1f} GB/s")
     if "iq2_k" in cells:
-        results["iq2_k"] = decode_cell(torch, device, "iq2_k", 8, args, seed=13)
+        results["iq2_k"] = decode_cell(torch, device, "iq2_k", 8, args, seed=13, windows=windows)
     if "iq1_s_r4" in cells:
-        results["iq1_s_r4"] = decode_cell(torch, device, "iq1_s_r4", 1, args, seed=17)
+        results["iq1_s_r4"] = decode_cell(torch, device, "iq1_s_r4", 1, args, seed=17, windows=windows)
+    del windows
+    torch.cuda.empty_cache()
+    if cells == ["headline"]:
+        cells = []
     if "dequant" in cells:
         results["dequant"] = {m: dequant_cell(torch, device, m, args, seed=19) for m in ("iq2_ks", "iq2_k", "iq1_s_r4")}
     if "prefill" in cells:
@@ -677,27 +782,53 @@ def main() -> int:
                 # HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE passes over `--probe`,
                 # each calibrated on a plain copy of known size
                 "traffic": traffic, "traffic_source": traffic_file.name if traffic else None}
+    # every priced cell: its ratios and the reference's gates
+    summary, gates = {}, {}
+    for m, r in results.items():
+        for c, cell in (r.get("cells") or {}).items():
+            key = f"{m}_{c}" + (f"_x{r['tokens']}" if r.get("tokens", 1) != 1 else "")
+            summary[key] = {k: cell[k] for k in ("x_floor", "x_stream", "x_floor_grid") if k in cell}
+            summary[key].update(us=cell["decode"]["median_us"], floor_us=cell["floor"]["median_us"],
+                                gb_per_s=cell["decode"]["gb_per_s"])
+            gates[key] = cell["gates"]
+    for m, r in (results.get("dequant") or {}).items():
+        for c, cell in r.items():
+            key = f"producer_{m}_{c}"
+            summary[key] = {"x_floor": cell["x_floor"], "us": cell["decode"]["median_us"],
+                            "floor_us": cell["floor"]["median_us"], "gb_per_s": cell["decode"]["gb_per_s"]}
+            gates[key] = cell["gates"]
+    if "prefill" in results:
+        pf = results["prefill"]
+        summary["prefill"] = {"producer_gb_per_s": pf["producer_gb_per_s"], "gemm_tflops": pf["gemm_tflops"],
+                              "fused_tflops": pf["fused_tflops"], "fused_mfma_utilisation": pf["fused_mfma_utilisation"],
+                              "gemm_mfma_utilisation": pf["mfma_utilisation"]}
     line = {
         "metric": "routed decode achieved HBM GB/s (IQ2_KS, 256 experts, top-6, 1 token: gate+up and down)",
         "value": round(head["gb_per_s"], 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(head["ms_per_step"], 5), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "i8",
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8x3/int32",
+        "arithmetic": "fp16 activations as three exact int8 byte planes per 32-element block (20-bit fixed "
+                      "point), int8 weights, int32 MFMA sums, f32 scale folds, fp16 out",
         "data": "synthetic: N(0,0.02) rows, U(0.1,1) imatrix, quantized by the package codec "
                 f"({args.distinct} distinct experts per projection, row-rotated to 256 distinct stacks)",
         "config": {"workload": "IQ2_KS routed decode, 256 experts, top-6, 1 token, gate/up [2048x4096] x2 "
                                "+ down [4096x2048]", "experts": EXPERTS, "top_k": TOP_K, "tokens": 1,
                    "bytes_per_step": head["bytes_per_step"]},
-        "x_floor": {m: {c: r["cells"][c]["x_floor"] for c in r["cells"]} for m, r in results.items()
-                    if "cells" in r},
         "roofline": roofline,
         "cpu_baseline": base,
-        "results": results,
+        "bars": {"decode_vs_own_floor": DECODE_BAR, "producer_vs_own_floor": PRODUCER_BAR,
+                 "floor_band_gb_s": list(FLOOR_BAND_GBS)},
+        "cells": summary,
+        "gates": gates,
+        "all_gates_pass": all(all(g.values()) for g in gates.values()),
         "elapsed_s": round(time.time() - t_start, 1),
     }
-    text = json.dumps(line)
+    full = dict(line, results=results)
     if args.json_out:
-        Path(args.json_out).write_text(json.dumps(line, indent=2) + "\n")
-    print(text, flush=True)
+        Path(args.json_out).write_text(json.dumps(full, indent=2) + "\n")
+    else:
+        log("results: " + json.dumps(results))
+    print(json.dumps(line), flush=True)
     return 0
 
 

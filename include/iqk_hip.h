@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define IQK_HIP_ABI_VERSION 4
+#define IQK_HIP_ABI_VERSION 5
 
 #define IQK_MEMBER_IQ2_KS 0
 #define IQK_MEMBER_IQ2_K 1
@@ -51,6 +51,10 @@ extern "C" {
 int iqk_hip_abi_version(void);
 // The hipError_t of the most recent IQK_ERR_LAUNCH on this thread (0 if none).
 int iqk_hip_last_error(void);
+// No counterpart in the reference (its kernels compile from source at run
+// time): a digest of the sources and flags this library was built from, so a
+// loader can refuse a stale build (NUL-terminated hex, static storage).
+const char *iqk_hip_source_hash(void);
 // Geometry guards, the ABI form of check_gemv_geometry / check_dequant_geometry
 // (reference: src/mlx_iqk/kernels.py:100-129): IQK_OK or the refusal code.
 int iqk_check_gemv_geometry(int member, int64_t in_features, int64_t out_features);
@@ -73,6 +77,23 @@ int iqk_gemv_floor(int member, int64_t in_features, int64_t out_features, int64_
                    const void *x, const void *const *streams, int n_streams,
                    const uint32_t *sel, uint32_t pairs_per_row, uint32_t mats,
                    void *y, void *stream);
+
+// IQ1_S_R4's floor as the reference prices it (bench/floors.py:14-17): the
+// deleted-decode floor with the decode's grid lookups kept -- the grid staged
+// in LDS and every entry the blocks index read, folded into the hash.  The
+// other members have no lookups: for them this is iqk_gemv_floor.  Same
+// arguments as iqk_gemv_floor.
+int iqk_gemv_floor_grid(int member, int64_t in_features, int64_t out_features, int64_t num_experts,
+                        const void *x, const void *const *streams, int n_streams,
+                        const uint32_t *sel, uint32_t pairs_per_row, uint32_t mats,
+                        void *y, void *stream);
+
+// The pure byte-stream floor of the pricing (no counterpart in the
+// reference's kernel seam; the reference prices against its deleted-decode
+// floors only): one dispatch that reads `bytes` contiguous bytes of src (16-byte
+// aligned, bytes a multiple of 16) with no expert-id read and no decode, and
+// writes a fold of them to out (u32 [ceil(bytes / 4096)], no meaningful values).
+int iqk_stream_floor(const void *src, uint64_t bytes, uint32_t *out, void *stream);
 
 // Decode GEMV over expert-sorted pairs, one workgroup per pair (replaces
 // gemv_sorted_kernel + IqkSwitchLinear.gemv_sorted,
@@ -144,7 +165,9 @@ int iqk_dequant_floor(int member, int64_t in_features, int64_t out_features, int
 // y: f16 [n_slots, out_features]; group_offsets: u32 [n_groups + 1] (device,
 // non-decreasing, last = n_slots); x_rows, y_rows: u32 [n_slots] (device;
 // y_rows NULL = identity, else a permutation of [0, n_slots)).  Device-side
-// indices out of range are skipped, never dereferenced.  in_features % 32 == 0;
+// indices out of range are never dereferenced: a slot whose x_rows entry is
+// >= n_x_rows gets a NaN output row, a y_rows entry >= n_slots is not
+// stored.  in_features % 32 == 0;
 // any out_features > 0.
 int iqk_grouped_gemm(int64_t in_features, int64_t out_features, int64_t n_groups, int64_t n_slots,
                      const void *x, int64_t n_x_rows, const void *w, const uint32_t *group_offsets,

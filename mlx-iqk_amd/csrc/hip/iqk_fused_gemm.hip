@@ -189,7 +189,7 @@ void fused_gemm_kernel(FusedArgs a) {
     __shared__ TileScan ts;
     __shared__ __attribute__((aligned(16))) uint8_t xs[2][kFusedBM * kXStride];
     // per slot of the tile: its output row, bit 31 set when its activations
-    // are real (else its output row is 0), or kNoStore
+    // are real (else its output row is NaN), or kNoStore
     __shared__ uint32_t slot_dst[kFusedBM];
     constexpr uint32_t kNoStore = 0x7fffffffu;  // above any row (n_slots <= 2^30)
     __shared__ __attribute__((aligned(16))) std::conditional_t<IQ1, FusedGrid, S> sc;
@@ -202,7 +202,7 @@ void fused_gemm_kernel(FusedArgs a) {
     if (!find_mtile<kFusedBM, kFusedThreads>(a.offs, a.n_groups, tile, ts, g, mtile)) return;  // surplus block
 
     // Offsets and row indices are device data: a slot outside [0, n_slots)
-    // is never stored, a row outside x is never read (its output row is 0),
+    // is never stored, a row outside x is never read (its output row is NaN),
     // and a weight row past out_features is never stored.  Loads of such
     // rows read an in-bounds row instead, so the step has no branches but
     // (IQ1_S_R4) the one that skips staging activation rows past the tile's
@@ -388,7 +388,7 @@ void fused_gemm_kernel(FusedArgs a) {
             const uint32_t dst = slot_dst[32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3)];
             if (dst != kNoStore)
                 a.y[size_t(dst & 0x7fffffffu) * a.N + n0 + lrow] =
-                    (dst >> 31) ? uint16_t(float_to_half_bits(acc[mb][r])) : uint16_t(0);
+                    (dst >> 31) ? uint16_t(float_to_half_bits(acc[mb][r])) : kHalfNaN;
         }
     }
 }

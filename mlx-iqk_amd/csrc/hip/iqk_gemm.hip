@@ -49,8 +49,9 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a) {
     uint32_t g, mtile;
     if (!find_mtile<kGemmBM>(a.offs, a.n_groups, blockIdx.x, ts, g, mtile)) return;  // surplus block
 
-    // Offsets and row indices are device data: any slot outside [0, n_slots)
-    // or row outside x is skipped (zero operand, no store), never read.
+    // Offsets and row indices are device data: a slot outside [0, n_slots)
+    // is never stored, and a row outside x is never read (zero operand; the
+    // slot's output row is NaN).
     const uint32_t gend = min(a.offs[g + 1], a.n_slots);
     const uint32_t m0 = a.offs[g] + mtile * kGemmBM;
     const int wave = tid / 64, lane = tid % 64;
@@ -115,10 +116,11 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a) {
             if (p >= gend) continue;
             const uint32_t yrow = a.yr ? a.yr[p] : p;
             if (yrow >= a.n_slots) continue;
+            const bool real = a.xr[p] < a.n_x_rows;  // else the row is NaN
             uint16_t *yp = a.y + size_t(yrow) * a.N + n0 + lr;  // only columns with bv[j] are stored
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                if (bv[j]) yp[16 * j] = uint16_t(float_to_half_bits(acc[i][j][r]));
+                if (bv[j]) yp[16 * j] = real ? uint16_t(float_to_half_bits(acc[i][j][r])) : kHalfNaN;
         }
     }
 }

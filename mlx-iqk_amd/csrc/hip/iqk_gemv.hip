@@ -297,7 +297,7 @@ int launch_gemv(int64_t n, const GemvArgs &a, uint32_t mats, hipStream_t st) {
 }
 
 // The int8-MFMA path (iqk_gemv_mfma.hip); -1 when it does not apply.
-int gemv_mfma_dispatch(bool floor, int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
+int gemv_mfma_dispatch(int floor, int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
                        int64_t n_x_rows, const void *const *streams, int n_streams, const uint32_t *sel,
                        const uint32_t *toks, bool union_runs, uint32_t pairs_per_row, uint32_t mats, void *y,
                        hipStream_t st);
@@ -307,7 +307,10 @@ int gemv_mfma_dispatch(bool floor, int member, int64_t n, int64_t out, int64_t n
 // beyond is a NaN output row) and union_runs picks the one-read-per-run form
 // where the MFMA path serves (the VALU path computes the same rows pair by
 // pair).
-template <bool FLOOR>
+// FLOOR: 0 the decode, 1 its deleted-decode floor, 2 that floor keeping
+// IQ1_S_R4's grid lookups (the VALU path, which has no staged grid, serves 2
+// as 1).
+template <int FLOOR>
 int gemv_entry(int member, int64_t n, int64_t out, int64_t num_experts, const void *x, int64_t n_x_rows,
                const void *const *streams, int n_streams, const uint32_t *sel, const uint32_t *toks,
                bool union_runs, uint32_t pairs_per_row, uint32_t mats, void *y, void *stream) {
@@ -339,9 +342,9 @@ int gemv_entry(int member, int64_t n, int64_t out, int64_t num_experts, const vo
     a.out_features = uint32_t(out);
     a.y = static_cast<uint16_t *>(y);
     switch (member) {
-        case IQK_MEMBER_IQ2_KS: return launch_gemv<IQ2_KS, FLOOR>(n, a, mats, st);
-        case IQK_MEMBER_IQ2_K: return launch_gemv<IQ2_K, FLOOR>(n, a, mats, st);
-        default: return launch_gemv<IQ1_S_R4, FLOOR>(n, a, mats, st);
+        case IQK_MEMBER_IQ2_KS: return launch_gemv<IQ2_KS, FLOOR != 0>(n, a, mats, st);
+        case IQK_MEMBER_IQ2_K: return launch_gemv<IQ2_K, FLOOR != 0>(n, a, mats, st);
+        default: return launch_gemv<IQ1_S_R4, FLOOR != 0>(n, a, mats, st);
     }
 }
 
@@ -360,7 +363,7 @@ int iqk_gemv(int member, int64_t n, int64_t out, int64_t num_experts, const void
              const void *const *streams, int n_streams, const uint32_t *sel, uint32_t pairs_per_row,
              uint32_t mats, void *y, void *stream) {
     const int64_t rows = pairs_per_row ? mats / pairs_per_row : 0;
-    return iqk::gemv_entry<false>(member, n, out, num_experts, x, rows, streams, n_streams, sel, nullptr, false,
+    return iqk::gemv_entry<0>(member, n, out, num_experts, x, rows, streams, n_streams, sel, nullptr, false,
                                   pairs_per_row, mats, y, stream);
 }
 
@@ -368,8 +371,16 @@ int iqk_gemv_floor(int member, int64_t n, int64_t out, int64_t num_experts, cons
                    const void *const *streams, int n_streams, const uint32_t *sel, uint32_t pairs_per_row,
                    uint32_t mats, void *y, void *stream) {
     const int64_t rows = pairs_per_row ? mats / pairs_per_row : 0;
-    return iqk::gemv_entry<true>(member, n, out, num_experts, x, rows, streams, n_streams, sel, nullptr, false,
+    return iqk::gemv_entry<1>(member, n, out, num_experts, x, rows, streams, n_streams, sel, nullptr, false,
                                  pairs_per_row, mats, y, stream);
+}
+
+int iqk_gemv_floor_grid(int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
+                        const void *const *streams, int n_streams, const uint32_t *sel, uint32_t pairs_per_row,
+                        uint32_t mats, void *y, void *stream) {
+    const int64_t rows = pairs_per_row ? mats / pairs_per_row : 0;
+    return iqk::gemv_entry<2>(member, n, out, num_experts, x, rows, streams, n_streams, sel, nullptr, false,
+                              pairs_per_row, mats, y, stream);
 }
 
 int iqk_gemv_sorted(int member, int64_t n, int64_t out, int64_t num_experts, const void *x, int64_t n_x_rows,
@@ -377,7 +388,7 @@ int iqk_gemv_sorted(int member, int64_t n, int64_t out, int64_t num_experts, con
                     uint32_t mats, void *y, void *stream) {
     if (member == IQK_MEMBER_IQ1_S_R4) return IQK_ERR_MEMBER;  // no sorted form
     if (!toks && mats) return IQK_ERR_ARGUMENT;
-    return iqk::gemv_entry<false>(member, n, out, num_experts, x, n_x_rows, streams, n_streams, sorted_ids, toks,
+    return iqk::gemv_entry<0>(member, n, out, num_experts, x, n_x_rows, streams, n_streams, sorted_ids, toks,
                                   false, 1u, mats, y, stream);
 }
 
@@ -386,7 +397,7 @@ int iqk_gemv_union(int member, int64_t n, int64_t out, int64_t num_experts, cons
                    uint32_t mats, void *y, void *stream) {
     if (member == IQK_MEMBER_IQ1_S_R4) return IQK_ERR_MEMBER;  // no union form
     if (!toks && mats) return IQK_ERR_ARGUMENT;
-    return iqk::gemv_entry<false>(member, n, out, num_experts, x, n_x_rows, streams, n_streams, sorted_ids, toks,
+    return iqk::gemv_entry<0>(member, n, out, num_experts, x, n_x_rows, streams, n_streams, sorted_ids, toks,
                                   true, 1u, mats, y, stream);
 }
 

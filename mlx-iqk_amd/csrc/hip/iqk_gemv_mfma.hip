@@ -610,6 +610,39 @@ struct LaneIq1s {
         return h;
     }
 
+    // Grid indices of the four 8-weight groups of block 4i + b, as the 16-bit
+    // halves of ix[0] (groups 0, 1) and ix[1] (groups 2, 3): low bytes of the
+    // index word placed by a v_perm, the 3-bit high fields of the qh word by
+    // one multiply that copies them to two places (bits 8 and 21 up; for
+    // groups 2, 3: 2 and 15 up): the copies do not overlap, so no carries,
+    // and the mask keeps exactly the wanted fields at bits 8-10 and 24-26.
+    __device__ __forceinline__ void grid_indices(int i, int b, uint32_t (&ix)[2]) const {
+        const uint32_t qw = qv[i][b];
+        const uint32_t hw = (qh[i][b >> 1] >> (16 * (b & 1))) & 0xfffu;  // four 3-bit high fields
+        ix[0] = (__umul24(hw, 0x200100u) & 0x07000700u) | perm(qw, qw, 0x0c010c00u);
+        ix[1] = (__umul24(hw, 0x008004u) & 0x07000700u) | perm(qw, qw, 0x0c030c02u);
+    }
+
+    // The decode's grid lookups without the decode: every entry its blocks
+    // index (two 8-byte LDS reads per 16 weights, the decode's addresses),
+    // folded into a hash.
+    __device__ __forceinline__ uint32_t grid_hash(const uint2_t *b8) const {
+        const uint8_t *b8b = reinterpret_cast<const uint8_t *>(b8);
+        uint32_t h = 0;
+#pragma unroll
+        for (int c = 0; c < 4 * NI; ++c) {
+            uint32_t ix[2];
+            grid_indices(c >> 2, c & 3, ix);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const uint2_t w0 = *reinterpret_cast<const uint2_t *>(b8b + lo16_x8(ix[t]));
+                const uint2_t w1 = *reinterpret_cast<const uint2_t *>(b8b + hi16_x8(ix[t]));
+                h += (2u * c + 5u) * (w0.x + 3u * w0.y) + (2u * c + 7u) * (w1.x + 5u * w1.y);
+            }
+        }
+        return h;
+    }
+
     // blocks 16i+4g+b (32 weights: index bytes of dword b of qv[i], qh word b
     // of qh[i]).  The table holds 8g + 1; a block with a negative shift uses
     // 8g - 1, which takes 2 sum(f) off its digit sum.  fsum2: 2 sum(f) of
@@ -666,17 +699,8 @@ struct LaneIq1s {
                 }
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const uint32_t qw = ln[r].qv[i][b];
-                    const uint32_t hw = (ln[r].qh[i][b >> 1] >> (16 * (b & 1))) & 0xfffu;  // four 3-bit high fields
-                    // Grid indices of groups 2t, 2t+1 as the 16-bit halves of
-                    // ix[t]: low bytes 2t, 2t+1 of qw placed by a v_perm, high
-                    // fields 2t, 2t+1 of hw by one multiply that copies hw to
-                    // two places (bits 8 and 21 up; for t = 1, 2 and 15 up):
-                    // the copies do not overlap, so no carries, and the mask
-                    // keeps exactly the wanted fields at bits 8-10 and 24-26.
-                    const uint32_t ix[2] = {
-                        (__umul24(hw, 0x200100u) & 0x07000700u) | perm(qw, qw, 0x0c010c00u),
-                        (__umul24(hw, 0x008004u) & 0x07000700u) | perm(qw, qw, 0x0c030c02u)};
+                    uint32_t ix[2];
+                    ln[r].grid_indices(i, b, ix);
 #pragma unroll
                     for (int t = 0; t < 2; ++t) {  // 8-weight groups 2t, 2t+1 of the block
                         const uint2_t w0 = *reinterpret_cast<const uint2_t *>(b8b + lo16_x8(ix[t]));
@@ -708,6 +732,11 @@ using LaneOf = std::conditional_t<MEMBER == IQ2_KS, LaneIq2ks<N>,
                                   std::conditional_t<MEMBER == IQ2_K, LaneIq2k<N>,
                                                      LaneIq1s<N, Gemv2Shape<MEMBER, N>::WK>>>;
 
+// What a launch computes: the decode, or one of its floors -- the decode's
+// loads with the decode deleted (kFloor), and for IQ1_S_R4 also that floor
+// with the decode's grid staging and lookups kept (kFloorGrid).
+enum GemvKind : int { kDecode = 0, kFloor = 1, kFloorGrid = 2 };
+
 // How a launch maps pairs to activation rows and stream reads.
 enum GemvMode : int {
     kPairs = 0,   // pair m reads x[m / pairs_per_row]; one workgroup per (tile, pair)
@@ -723,7 +752,7 @@ enum GemvMode : int {
 // share every A read, so a workgroup stages its activations for 64 rows;
 // five wavefronts per SIMD.  kUnion re-expands a lane's stream words for
 // each pair of its run (the words are read once); five wavefronts per SIMD.
-template <int MEMBER, int N, bool FLOOR, int MODE, int R>
+template <int MEMBER, int N, int FLOOR, int MODE, int R>
 __global__ __launch_bounds__((Gemv2Shape<MEMBER, N>::THREADS))
 __attribute__((amdgpu_waves_per_eu(MODE == kUnion || R == 2 ? 5 : 6)))
 void gemv_mfma_kernel(Gemv2Args a) {
@@ -783,11 +812,11 @@ void gemv_mfma_kernel(Gemv2Args a) {
     load_x(x_ok ? tok : 0u, xv);
     constexpr bool IQ1 = MEMBER == IQ1_S_R4;
     // IQ1_S_R4: the codes of grid entries 4tid .. 4tid+3
-    constexpr bool GRID = IQ1 && !FLOOR;
+    constexpr bool GRID = IQ1 && FLOOR != kFloor;
     static_assert(!IQ1 || IQK_IQ1S_GRID_SIZE == 4 * S::THREADS, "four grid entries per thread");
     uint2_t gridc = {0u, 0u};
     if constexpr (GRID) gridc = reinterpret_cast<const uint2_t *>(iqk_iq1s_grid_codes)[tid];
-    constexpr bool KTAB = MEMBER == IQ2_K && !FLOOR;
+    constexpr bool KTAB = MEMBER == IQ2_K && FLOOR == kDecode;
     uint2_t ktv = {0u, 0u};
     if (KTAB && tid < 32) ktv = reinterpret_cast<const uint2_t *>(kIq2kTab.w)[tid];
 
@@ -817,10 +846,20 @@ void gemv_mfma_kernel(Gemv2Args a) {
             }
         }
         float acc[R];
-        if constexpr (FLOOR) {
+        if constexpr (FLOOR != kDecode) {
             uint32_t h = xv.x + 3u * xv.y + 5u * xv.z + 7u * xv.w;
 #pragma unroll
             for (int r = 0; r < R; ++r) h += lane[r].hash();
+            if constexpr (GRID) {  // kFloorGrid: the grid staging and every lookup
+                uint4_t g0, g1;
+                expand_grid_pair(gridc.x, g0);
+                expand_grid_pair(gridc.y, g1);
+                reinterpret_cast<uint4_t *>(sm.b8)[2 * tid] = g0;
+                reinterpret_cast<uint4_t *>(sm.b8)[2 * tid + 1] = g1;
+                __syncthreads();
+#pragma unroll
+                for (int r = 0; r < R; ++r) h += lane[r].grid_hash(sm.b8);
+            }
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[r] = float((h >> r) & 0xffu);
         } else {
@@ -883,7 +922,7 @@ void gemv_mfma_kernel(Gemv2Args a) {
     }
 }
 
-template <int MEMBER, bool FLOOR, int MODE, int R>
+template <int MEMBER, int FLOOR, int MODE, int R>
 int launch_gemv_mfma(int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t st) {
     const uint32_t groups = a.out_features / (kGroupRows * R);
     const dim3 grid = MODE == kPairs ? dim3{groups, a.pairs_per_row, mats / a.pairs_per_row} : dim3{groups, 1u, mats};
@@ -895,7 +934,7 @@ int launch_gemv_mfma(int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t s
     return record_launch(hipGetLastError());
 }
 
-template <bool FLOOR, int MODE, int R>
+template <int FLOOR, int MODE, int R>
 int launch_member(int member, int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t st) {
     switch (member) {
         case IQK_MEMBER_IQ2_KS: return launch_gemv_mfma<IQ2_KS, FLOOR, MODE, R>(n, a, mats, st);
@@ -921,7 +960,7 @@ constexpr uint64_t kTwoRowMinGroupsIq2 = 8 * 768;
 // path does not apply.  `toks` NULL = pairs mode (x row m / pairs_per_row);
 // else x row toks[m] of n_x_rows, and `union_runs` selects the one-read-per-
 // run form.
-int gemv_mfma_dispatch(bool floor, int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
+int gemv_mfma_dispatch(int floor, int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
                        int64_t n_x_rows, const void *const *streams, int n_streams, const uint32_t *sel,
                        const uint32_t *toks, bool union_runs, uint32_t pairs_per_row, uint32_t mats, void *y,
                        hipStream_t st) {
@@ -949,15 +988,24 @@ int gemv_mfma_dispatch(bool floor, int member, int64_t n, int64_t out, int64_t n
         const bool two = out % (2 * kGroupRows) == 0 &&
                          (member == IQK_MEMBER_IQ1_S_R4 ? groups >= kTwoRowMinGroups
                                                         : n == 2048 && groups >= kTwoRowMinGroupsIq2);
-        if (two)
-            return floor ? launch_member<true, kPairs, 2>(member, n, a, mats, st)
-                         : launch_member<false, kPairs, 2>(member, n, a, mats, st);
-        return floor ? launch_member<true, kPairs, 1>(member, n, a, mats, st)
-                     : launch_member<false, kPairs, 1>(member, n, a, mats, st);
+        // only IQ1_S_R4 has grid lookups to keep; the others' kFloorGrid is kFloor
+        const int kind = floor == kFloorGrid && member != IQK_MEMBER_IQ1_S_R4 ? kFloor : floor;
+        if (two) {
+            switch (kind) {
+                case kFloor: return launch_member<kFloor, kPairs, 2>(member, n, a, mats, st);
+                case kFloorGrid: return launch_member<kFloorGrid, kPairs, 2>(member, n, a, mats, st);
+                default: return launch_member<kDecode, kPairs, 2>(member, n, a, mats, st);
+            }
+        }
+        switch (kind) {
+            case kFloor: return launch_member<kFloor, kPairs, 1>(member, n, a, mats, st);
+            case kFloorGrid: return launch_member<kFloorGrid, kPairs, 1>(member, n, a, mats, st);
+            default: return launch_member<kDecode, kPairs, 1>(member, n, a, mats, st);
+        }
     }
-    if (floor) return IQK_ERR_ARGUMENT;
-    return union_runs ? launch_member<false, kUnion, 1>(member, n, a, mats, st)
-                      : launch_member<false, kSorted, 1>(member, n, a, mats, st);
+    if (floor != kDecode) return IQK_ERR_ARGUMENT;
+    return union_runs ? launch_member<kDecode, kUnion, 1>(member, n, a, mats, st)
+                      : launch_member<kDecode, kSorted, 1>(member, n, a, mats, st);
 }
 
 }  // namespace iqk

@@ -7,12 +7,13 @@ Loading never falls back to anything: a missing or stale library raises
 from __future__ import annotations
 
 import ctypes
-from ctypes import c_int, c_int64, c_uint32, c_void_p
+from ctypes import c_char_p, c_int, c_int64, c_uint32, c_void_p
 from pathlib import Path
 
+from . import build
 from .build import HIP_LIB
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 OK, ERR_MEMBER, ERR_GEOMETRY, ERR_ARGUMENT, ERR_LAUNCH = 0, 1, 2, 3, 4
 _CODES = {ERR_MEMBER: "unknown member", ERR_GEOMETRY: "unsized geometry",
@@ -27,12 +28,16 @@ _i32p = ctypes.POINTER(ctypes.c_int32)
 SIGNATURES = {
     "iqk_hip_abi_version": (c_int, []),
     "iqk_hip_last_error": (c_int, []),
+    "iqk_hip_source_hash": (c_char_p, []),
     "iqk_check_gemv_geometry": (c_int, [c_int, c_int64, c_int64]),
     "iqk_check_dequant_geometry": (c_int, [c_int, c_int64, c_int64]),
     "iqk_gemv": (c_int, [c_int, c_int64, c_int64, c_int64, c_void_p, ctypes.POINTER(c_void_p), c_int,
                          c_void_p, c_uint32, c_uint32, c_void_p, c_void_p]),
     "iqk_gemv_floor": (c_int, [c_int, c_int64, c_int64, c_int64, c_void_p, ctypes.POINTER(c_void_p), c_int,
                                c_void_p, c_uint32, c_uint32, c_void_p, c_void_p]),
+    "iqk_gemv_floor_grid": (c_int, [c_int, c_int64, c_int64, c_int64, c_void_p, ctypes.POINTER(c_void_p), c_int,
+                                    c_void_p, c_uint32, c_uint32, c_void_p, c_void_p]),
+    "iqk_stream_floor": (c_int, [c_void_p, ctypes.c_uint64, c_void_p, c_void_p]),
     "iqk_gemv_sorted": (c_int, [c_int, c_int64, c_int64, c_int64, c_void_p, c_int64, ctypes.POINTER(c_void_p),
                                 c_int, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p]),
     "iqk_gemv_union": (c_int, [c_int, c_int64, c_int64, c_int64, c_void_p, c_int64, ctypes.POINTER(c_void_p),
@@ -79,6 +84,11 @@ def load() -> ctypes.CDLL:
     if lib.iqk_hip_abi_version() != ABI_VERSION:
         raise IqkNativeError(
             f"{path} has ABI {lib.iqk_hip_abi_version()}, this package expects {ABI_VERSION}; rebuild it")
+    built, current = lib.iqk_hip_source_hash().decode(), build.hip_source_hash()
+    if built != current:
+        raise IqkNativeError(
+            f"{path} was built from other sources (digest {built}, sources now {current}); "
+            "rebuild it with `python -m mlx_iqk_amd.build`")
     _LIB = lib
     return lib
 

@@ -10,6 +10,7 @@ both.
 
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -36,6 +37,7 @@ HIP_SOURCES = {
     "iqk_gemm.hip": (),
     "iqk_fused_gemm.hip": (),
     "iqk_pack.hip": (),
+    "iqk_floor.hip": (),
 }
 OFFLOAD_ARCH = "gfx950"
 
@@ -60,10 +62,28 @@ def codec_command(out: Path = CODEC_LIB) -> list[str]:
             "-o", str(out), str(CSRC / "codec" / "iqk_codec.cpp")]
 
 
-def hip_object_command(source: str, obj: Path) -> list[str]:
+def hip_source_files() -> list[Path]:
+    """Every file the kernel library is compiled from."""
+    return sorted([*(CSRC / "hip").glob("*.hip"), *(CSRC / "hip").glob("*.h"), CSRC / "iq1s_grid.h",
+                   INCLUDE / "iqk_hip.h"])
+
+
+def hip_source_hash() -> str:
+    """A digest of the kernel library's sources and compile flags.  It is
+    compiled into the library (``iqk_hip_source_hash``), so a loader can tell a
+    library built from other sources -- a stale build -- from a current one."""
+    h = hashlib.sha256()
+    for f in hip_source_files():
+        h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
+    h.update(repr(sorted(HIP_SOURCES.items())).encode() + OFFLOAD_ARCH.encode())
+    return h.hexdigest()[:16]
+
+
+def hip_object_command(source: str, obj: Path, source_hash: str = "") -> list[str]:
     return [_hipcc(), f"--offload-arch={OFFLOAD_ARCH}", "-O3", "-fPIC", "-std=c++17",
             # packed fp32 VALU ops stay off: hand the compiler no v_pk_*_f32
             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+            f'-DIQK_SOURCE_HASH="{source_hash or hip_source_hash()}"',
             *HIP_SOURCES[source], f"-I{INCLUDE}", "-c", "-o", str(obj), str(CSRC / "hip" / source)]
 
 
@@ -86,8 +106,9 @@ def build_hip() -> Path:
     tmp = HIP_LIB.with_suffix(".so.tmp")
     with tempfile.TemporaryDirectory(prefix="iqk_hip_") as work:
         objects = [Path(work) / (Path(s).stem + ".o") for s in HIP_SOURCES]
+        digest = hip_source_hash()
         procs = [(cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True))
-                 for cmd in (hip_object_command(s, o) for s, o in zip(HIP_SOURCES, objects))]
+                 for cmd in (hip_object_command(s, o, digest) for s, o in zip(HIP_SOURCES, objects))]
         failures = []
         for cmd, proc in procs:
             out, err = proc.communicate()

@@ -38,10 +38,11 @@ def check_gemv_geometry(in_features: int, out_features: int) -> tuple[int, int]:
     n = check_row_width(in_features)
     if n not in SUPPORTED_IN_FEATURES:
         raise IqkKernelError(
-            f"the decode gemv is sized per input width and covers {SUPPORTED_IN_FEATURES}, got {in_features}")
+            f"no decode GEMV is compiled for in_features={in_features} (widths: {SUPPORTED_IN_FEATURES})")
     out = int(out_features)
     if out <= 0 or out % ROWS_PER_TG:
-        raise IqkKernelError(f"out_features {out_features} is not a positive multiple of {ROWS_PER_TG}")
+        raise IqkKernelError(f"the decode GEMV writes rows in tiles of {ROWS_PER_TG}; "
+                             f"out_features={out_features} does not fill whole tiles")
     return n, out
 
 
@@ -49,10 +50,10 @@ def check_dequant_geometry(in_features: int, out_features: int) -> tuple[int, in
     n = check_row_width(in_features)
     if n not in SUPPORTED_IN_FEATURES:
         raise IqkKernelError(
-            f"the dequantization is sized per input width and covers {SUPPORTED_IN_FEATURES}, got {in_features}")
+            f"no producer is compiled for in_features={in_features} (widths: {SUPPORTED_IN_FEATURES})")
     out = int(out_features)
     if out <= 0:
-        raise IqkKernelError(f"out_features {out_features} is not positive")
+        raise IqkKernelError(f"out_features must be at least 1, got {out_features}")
     return n, out
 
 
@@ -107,12 +108,13 @@ def check_streams(member: str, streams: list[torch.Tensor], num_experts: int, ou
 
 
 def gemv(member: str, x: torch.Tensor, streams: list[torch.Tensor], sel: torch.Tensor, pairs_per_row: int,
-         num_experts: int, out_features: int, *, floor: bool = False,
+         num_experts: int, out_features: int, *, floor: bool | str = False,
          out: torch.Tensor | None = None) -> torch.Tensor:
     """Decode GEMV: ``y[m] = W[sel[m]] @ x[m // pairs_per_row]``, fp16 ``[mats, out]``.
 
     ``x`` is fp16 ``[rows, in]``, ``sel`` int32/uint32 ``[mats]`` on the same
-    GPU.  ``floor=True`` runs the deleted-decode floor instead.
+    GPU.  ``floor=True`` runs the deleted-decode floor instead, ``floor="grid"``
+    that floor with IQ1_S_R4's grid lookups kept (the reference's IQ1 floor).
     """
     check_member(member)
     n = int(x.shape[-1])
@@ -135,7 +137,7 @@ def gemv(member: str, x: torch.Tensor, streams: list[torch.Tensor], sel: torch.T
     if mats == 0:
         return out
     lib = _native.load()
-    fn = lib.iqk_gemv_floor if floor else lib.iqk_gemv
+    fn = lib.iqk_gemv_floor_grid if floor == "grid" else lib.iqk_gemv_floor if floor else lib.iqk_gemv
     ptrs = _native.pointer_array([t.data_ptr() for t in streams])
     # gridDim.y carries the pair index: launch in pair chunks that keep whole
     # activation rows together.
@@ -150,12 +152,32 @@ def gemv(member: str, x: torch.Tensor, streams: list[torch.Tensor], sel: torch.T
     return out
 
 
+def stream_floor(src: torch.Tensor, nbytes: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """The pure byte-stream floor: one dispatch reading the first ``nbytes`` of
+    ``src`` (any contiguous GPU tensor, 16-byte aligned; ``nbytes`` a multiple of
+    16), with no expert-id read and no decode.  Returns the dispatch's output
+    words (u32 ``[ceil(nbytes / 4096)]``, no meaningful values)."""
+    if not isinstance(src, torch.Tensor) or src.device.type != "cuda" or not src.is_contiguous():
+        raise IqkKernelError("src must be a contiguous GPU tensor")
+    nbytes = int(nbytes)
+    if nbytes <= 0 or nbytes % 16 or nbytes > src.numel() * src.element_size():
+        raise IqkKernelError(f"{nbytes} bytes is not a positive multiple of 16 within src")
+    words = (nbytes + 4095) // 4096
+    if out is None:
+        out = torch.empty(words, dtype=torch.int32, device=src.device)
+    elif out.numel() < words or out.dtype not in (torch.int32, torch.uint32) or out.device != src.device:
+        raise IqkKernelError(f"out must hold {words} 32-bit words on {src.device}")
+    rc = _native.load().iqk_stream_floor(src.data_ptr(), nbytes, out.data_ptr(), _stream_ptr(src.device))
+    _native.check(rc, f"iqk_stream_floor({nbytes})")
+    return out
+
+
 def check_iq2_member(member: str) -> str:
     """Members the sorted and union GEMVs cover (reference: src/mlx_iqk/kernels.py:89-97)."""
     check_member(member)
     if member not in IQ2_MEMBERS:
         raise IqkKernelError(
-            f"the sorted and union decode GEMVs cover {IQ2_MEMBERS}; {member!r} has no such variant")
+            f"{member!r} has no expert-sorted GEMV; those forms exist for {IQ2_MEMBERS}")
     return member
 
 
@@ -377,6 +399,6 @@ __all__ = [
     "DEQUANT_THREADS", "IQ2_MEMBERS", "MEMBERS", "ROWS_PER_TG",
     "SUPPORTED_IN_FEATURES", "TABLE_INPUT_NAMES", "WEIGHTS_PER_LANE", "IqkKernelError",
     "check_dequant_geometry", "check_gemv_geometry", "check_streams", "dequant", "dequant_input_names",
-    "FUSED_MEMBERS", "check_iq2_member", "fused_matmul", "gemv", "pack", "gemv_input_names", "gemv_sorted", "grouped_gemm",
+    "FUSED_MEMBERS", "check_iq2_member", "fused_matmul", "gemv", "pack", "stream_floor", "gemv_input_names", "gemv_sorted", "grouped_gemm",
     "stream_dtypes",
 ]

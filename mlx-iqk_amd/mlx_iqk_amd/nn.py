@@ -7,11 +7,15 @@ same route choice (src/mlx_iqk/nn.py:49, 221-238):
 
 * **decode** (``indices.numel() <= DECODE_MAT_LIMIT`` and not sorted): the
   fused GEMV streams the selected experts' relayout directly;
-* **prefill** (otherwise): the producer reconstructs each routed expert once,
-  bit-exact, into fp16, and a sorted grouped fp16 MFMA GEMM contracts it.
-  The reference dequantizes every expert and calls ``mx.gather_mm``; here
-  only the routed experts are reconstructed, and the pair sort, grouping and
-  un-permute happen on the device with no host synchronisation.
+* **prefill** (otherwise): by default the fused contraction forms each
+  routed expert's fp16 weights -- the producer's values, bit for bit --
+  inside an fp16 MFMA grouped GEMM and never stores them
+  (``fused_prefill = True``); with ``fused_prefill = False`` the producer
+  reconstructs each routed expert once into an fp16 stack and a sorted
+  grouped GEMM contracts it.  The reference dequantizes every expert and
+  calls ``mx.gather_mm``; here only the routed experts are touched, and the
+  pair sort, grouping and un-permute happen on the device with no host
+  synchronisation.
 
 Shapes follow the reference: gate/up pass ``x [..., 1, 1, in]`` (one row per
 token shared by its ``top_k`` experts), down passes ``x [..., top_k, 1, in]``
@@ -71,7 +75,8 @@ def member_table(member: str, device=None) -> torch.Tensor:
 
 
 class IqkSwitchLinear(torch.nn.Module):
-    """Stacked IQ_K experts for one projection, ``(x, indices)`` interface."""
+    """One routed projection: ``num_experts`` IQ_K-quantized ``[out, in]`` matrices
+    held as relayout stream buffers, called with ``(x, indices)``."""
 
     mode = "iqk"
     fused_prefill = True
@@ -89,7 +94,7 @@ class IqkSwitchLinear(torch.nn.Module):
         self.out_features = int(out_features)
         self.in_features = int(in_features)
         if self.num_experts <= 0:
-            raise IqkRuntimeError(f"num_experts {num_experts} is not positive")
+            raise IqkRuntimeError(f"a stack needs at least one expert (num_experts={num_experts})")
         dtypes = stream_dtypes(member)
         for name, shape in component_shapes(member, num_experts, out_features, in_features).items():
             self.register_buffer(name, torch.zeros(shape, dtype=dtypes[name], device=device))
@@ -112,7 +117,8 @@ class IqkSwitchLinear(torch.nn.Module):
         """
         shapes = component_shapes(self.member, self.num_experts, self.out_features, self.in_features)
         if set(streams) != set(shapes):
-            raise IqkRuntimeError(f"{self.member} needs streams {sorted(shapes)}, got {sorted(streams)}")
+            raise IqkRuntimeError(f"stream set mismatch for {self.member}: expected {sorted(shapes)}, "
+                                  f"received {sorted(streams)}")
         dtypes = stream_dtypes(self.member)
         staged = {}
         for name, want in shapes.items():
@@ -122,8 +128,8 @@ class IqkSwitchLinear(torch.nn.Module):
             got = tuple(value.shape)
             if got != want:
                 raise IqkRuntimeError(
-                    f"stream {name} must be {want} for "
-                    f"{self.num_experts}x{self.out_features}x{self.in_features}, got {got}")
+                    f"stream {name} has shape {got}; a {self.num_experts}-expert "
+                    f"{self.out_features}x{self.in_features} stack needs {want}")
             if value.dtype != dtypes[name]:
                 raise IqkRuntimeError(f"stream {name} must be {dtypes[name]}, got {value.dtype}")
             staged[name] = value
@@ -169,10 +175,10 @@ class IqkSwitchLinear(torch.nn.Module):
 
     def _check_range(self, start: int, rows: int) -> None:
         if rows <= 0 or rows & (rows - 1):
-            raise IqkRuntimeError(f"range rows {rows} is not a positive power of two")
+            raise IqkRuntimeError(f"a row range spans a power-of-two count of rows, not {rows}")
         if start < 0 or start + rows > self.out_features:
             raise IqkRuntimeError(
-                f"range [{start}, {start + rows}) is outside out_features {self.out_features}")
+                f"rows [{start}, {start + rows}) do not lie within the {self.out_features} rows of an expert")
 
     # -- call -------------------------------------------------------------------
 
@@ -186,7 +192,7 @@ class IqkSwitchLinear(torch.nn.Module):
         """Fused GEMV over the selected experts; valid for any pair count
         (reference: src/mlx_iqk/nn.py:240-271)."""
         xt = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
-        sel = indices.reshape(-1).to(torch.int32).contiguous()
+        sel = self._device_ids(indices)
         mats, rows = int(sel.numel()), int(xt.shape[0])
         # Pairs sharing one activation row: top_k for gate/up, 1 for down.
         if rows <= 0 or mats % rows:
@@ -222,16 +228,27 @@ class IqkSwitchLinear(torch.nn.Module):
         return kernels.gemv_sorted(self.member, xt, self._streams(), sel, tok, self.num_experts,
                                    self.out_features, union=True)
 
+    def _device_ids(self, indices: torch.Tensor) -> torch.Tensor:
+        """Expert ids as the kernels read them (32-bit, compared unsigned with
+        num_experts, so a negative id is out of range).  Wider integers are
+        clamped to [-1, num_experts] first, so no out-of-range id wraps into
+        the stack."""
+        flat = indices.reshape(-1)
+        if flat.dtype not in (torch.int32, torch.uint32):
+            flat = torch.clamp(flat.to(torch.int64), -1, self.num_experts)
+        return flat.to(torch.int32).contiguous()
+
     def _sorted_operands(self, x, sorted_ids, toks):
         xt = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
-        sel = sorted_ids.reshape(-1).to(torch.int32).contiguous()
+        sel = self._device_ids(sorted_ids)
         tok = toks.reshape(-1).to(device=sel.device, dtype=torch.int32).contiguous()
         if tok.numel() != sel.numel():
             raise IqkRuntimeError(f"toks carries {tok.numel()} rows for {sel.numel()} pairs")
         return xt, sel, tok
 
     def prefill(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
-        """Producer + sorted grouped GEMM; the dequantized route of ``forward``.
+        """The prefill route of ``forward``: the fused contraction
+        (``fused_prefill``, the default), else producer + sorted grouped GEMM.
 
         Broadcasting follows ``gather_mm(x, W^T, rhs_indices=indices)``: the
         batch shape is ``broadcast(x.shape[:-2], indices.shape)`` and each pair
@@ -261,11 +278,19 @@ class IqkSwitchLinear(torch.nn.Module):
         xbatch = tuple(xb.shape[:-2])
         xflat = xb.reshape(-1, self.in_features).contiguous()
         xidx = torch.arange(math.prod(xbatch), device=device).reshape(xbatch).broadcast_to(batch).reshape(-1)
-        ids = indices.to(device=device, dtype=torch.int64).broadcast_to(batch).reshape(-1)
+        raw = indices.to(device=device, dtype=torch.int64).broadcast_to(batch).reshape(-1)
         E = self.num_experts
+        # An id outside [0, E) must reach no index op below (ROCm builds drop
+        # torch's device-side bounds asserts): its pair is grouped with expert
+        # 0 and given an activation row beyond x, which the kernels never read
+        # and answer with a NaN output row -- what the decode route returns.
+        valid = (raw >= 0) & (raw < E)
+        ids = torch.where(valid, raw, torch.zeros_like(raw))
         order = torch.argsort(ids, stable=True)
         r = torch.arange(M, device=device)
-        x_rows = (xidx[order][:, None] * M + r).reshape(-1).to(torch.int32)
+        no_row = torch.full_like(xidx, xflat.shape[0])
+        x_rows = (torch.where(valid, xidx, no_row)[order][:, None] * M + r).reshape(-1)
+        x_rows = torch.clamp(x_rows, max=xflat.shape[0]).to(torch.int32)
         y_rows = (order[:, None] * M + r).reshape(-1).to(torch.int32)
         if self.fused_prefill and self.member in kernels.FUSED_MEMBERS:
             counts = torch.zeros(E, dtype=torch.int64, device=device).index_add_(0, ids, torch.full_like(ids, M))

@@ -87,6 +87,19 @@ def test_entry_points_refuse_bad_arguments_before_launching(lib):
     assert lib.iqk_hip_last_error() == 0
 
 
+def test_library_carries_the_digest_of_its_sources(lib):
+    assert lib.iqk_hip_source_hash().decode() == build.hip_source_hash()
+
+
+def test_a_library_built_from_other_sources_is_refused(monkeypatch, lib):
+    """A stale build (sources edited after it was compiled) never runs: the
+    digest compiled into it no longer matches the sources beside it."""
+    monkeypatch.setattr(_native, "_LIB", None)
+    monkeypatch.setattr(build, "hip_source_hash", lambda: "0" * 16)
+    with pytest.raises(_native.IqkNativeError, match="other sources"):
+        _native.load()
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_native, "_LIB", None)
     monkeypatch.setattr(_native, "library_path", lambda: tmp_path / "absent.so")

@@ -143,6 +143,39 @@ def test_prefill_route_serves_the_sorted_pair_operand(device, member):
     assert _rel(got, oracle.prefill_reference(ref, x, idx)) < 3e-3
 
 
+@pytest.mark.parametrize("fused", (True, False))
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+def test_prefill_marks_out_of_range_experts_with_nan(device, member, fused):
+    """Ids outside [0, num_experts) -- the stack size, -1, and an int64 id past
+    2^32 that would wrap into range as 32 bits -- reach no index op: their
+    pairs come back as NaN rows, as on the decode route, and every other
+    pair is unaffected.  Both prefill routes, unsorted routing."""
+    n = 2048
+    module, ref = _module(member, n, 211, device)
+    rng = np.random.default_rng(213)
+    tokens, top_k = 20, 4
+    x = rng.standard_normal((tokens, 1, 1, n)).astype(np.float16)
+    idx = rng.integers(0, EXPERTS, size=(tokens, top_k)).astype(np.int64)
+    bad = np.zeros_like(idx, dtype=bool)
+    for (t, k), e in (((3, 1), EXPERTS), ((7, 0), -1), ((11, 3), 2 ** 32 + 1), ((19, 3), EXPERTS + 100)):
+        idx[t, k] = e
+        bad[t, k] = True
+    assert idx.size > DECODE_MAT_LIMIT
+    module.fused_prefill = fused
+    try:
+        got = module(torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device))
+    finally:
+        module.fused_prefill = True
+    got = got.float().cpu().numpy()
+    assert np.all(np.isnan(got[bad])) and not np.any(np.isnan(got[~bad]))
+    want = oracle.prefill_reference(ref, x, np.where(bad, 0, idx))
+    keep = got[~bad].astype(np.float64)
+    assert np.max(np.abs(keep - want[~bad])) / np.max(np.abs(want[~bad])) < 3e-3
+    # the decode route: the same ids, 32-bit wrap included, give NaN rows too
+    dec = module(torch.from_numpy(x[:12]).to(device), torch.from_numpy(idx[:12]).to(device)).float().cpu().numpy()
+    assert np.all(np.isnan(dec[bad[:12]])) and not np.any(np.isnan(dec[~bad[:12]]))
+
+
 @pytest.mark.parametrize("member", fmt.MEMBERS)
 def test_the_two_routes_agree_on_the_same_dispatch(device, member):
     n = 2048
