@@ -258,6 +258,8 @@ def decode_cell(torch, device, member: str, tokens: int, args, seed: int, want_s
             res["x_floor_grid"] = round(res["decode"]["median_us"] / res["floor_grid"]["median_us"], 4)
         res["ideal_us_at_8tbps"] = round(nbytes / HBM_PEAK_GBS / 1e3, 3)
         res["gates"] = gate_cell(res, DECODE_BAR)
+        if "floor_grid" in arms:  # the reference's IQ1_S_R4 floor keeps the grid lookups (bench/floors.py:14-17)
+            res["within_bar_vs_grid_floor"] = bool(res["x_floor_grid"] <= DECODE_BAR)
         cells[name] = res
         log(f"  {name:8s} decode {res['decode']['median_us']:8.2f} us ({res['decode']['gb_per_s']:7.1f} GB/s)"
             f"  floor {res['floor']['median_us']:8.2f} us  x{res['x_floor']:.3f}"
@@ -419,6 +421,22 @@ def prefill_cell(torch, device, args, seed: int):
                 b.synchronize()
                 times[key].append(a.elapsed_time(b) * 1e3 / burst)
         med = {k: statistics.median(v) for k, v in times.items()}
+        # the whole module call (the route's device-side bookkeeping + the fused kernel): GPU time
+        # from events around `burst` calls, host time per call from the wall clock
+        mod_gpu, mod_host = [], []
+        for _ in range(reps):
+            a, b = ev(), ev()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            a.record()
+            for _ in range(burst):
+                mod(xin, ids, sorted_indices=True)
+            b.record()
+            t1 = time.perf_counter()
+            b.synchronize()
+            mod_gpu.append(a.elapsed_time(b) * 1e3 / burst)
+            mod_host.append((t1 - t0) * 1e6 / burst)
+        med["module"], med["module_host"] = statistics.median(mod_gpu), statistics.median(mod_host)
         kernels.dequant(member, mod._streams(), EXPERTS, out, n, slot_of_expert=slot, n_slots=n_slots, out=w)
         yp = kernels.grouped_gemm(xin.reshape(-1, n), w, offs, rows).float()  # the producer route's output
         fused_dev = ((yf.float() - yp).abs().max() / yp.abs().max()).item()
@@ -432,14 +450,16 @@ def prefill_cell(torch, device, args, seed: int):
              "gemm_us": round(med["gemm"], 2), "gemm_flop": flop,
              "gemm_tflops": round(flop / (med["gemm"] * 1e-6) / 1e12, 2)}
         r["mfma_utilisation"] = round(r["gemm_tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
-        r.update({"fused_us": round(med["fused"], 2), "fused_tflops": round(flop / (med["fused"] * 1e-6) / 1e12, 2),
+        r.update({"module_forward_us": round(med["module"], 2), "module_forward_host_us": round(med["module_host"], 2),
+                  "fused_us": round(med["fused"], 2), "fused_tflops": round(flop / (med["fused"] * 1e-6) / 1e12, 2),
                   "fused_speedup_over_producer_route": round((med["producer"] + med["gemm"]) / med["fused"], 2),
                   "fused_max_dev_vs_producer_route": round(fused_dev, 6)})
         r["fused_mfma_utilisation"] = round(r["fused_tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
         res["projections"][name] = r
         log(f"  {name}: producer {med['producer']:.1f} us ({r['producer_gb_per_s']} GB/s, x{r['producer_x_floor']})"
             f"  gemm {med['gemm']:.1f} us ({r['gemm_tflops']} TFLOP/s)"
-            f"  fused {med['fused']:.1f} us ({r['fused_tflops']} TFLOP/s, dev {fused_dev:.2e})")
+            f"  fused {med['fused']:.1f} us ({r['fused_tflops']} TFLOP/s, dev {fused_dev:.2e})"
+            f"  module forward {med['module']:.1f} us GPU, {med['module_host']:.1f} us host")
         del mod, w, y, yf, yp
         torch.cuda.empty_cache()
         if name.startswith("gate_"):  # outside the prefill configuration's totals
@@ -470,11 +490,14 @@ def verify_cell(torch, device, args, seed: int):
     rb = fmt.ik_row_bytes(member, n)
     rng = np.random.default_rng(seed)
     res = {"member": member, "geometry": [out, n]}
-    for tokens in (8, 32):
+    for tokens, pool in ((8, None), (32, None), (8, 9)):
         variants = 16
         V = []
         for _ in range(variants):
-            idx = np.stack([rng.choice(EXPERTS, TOP_K, replace=False) for _ in range(tokens)]).astype(np.int32)
+            # uniform top-6 per token, or (pool) every token's top-6 from the same few experts: the
+            # speculative-verify shape, where runs of one expert are long
+            src = rng.choice(EXPERTS, pool, replace=False) if pool else np.arange(EXPERTS)
+            idx = np.stack([rng.choice(src, TOP_K, replace=False) for _ in range(tokens)]).astype(np.int32)
             flat = idx.reshape(-1)
             order = np.argsort(flat, kind="stable")
             V.append({"x": torch.randn(tokens, n, device=device).to(torch.float16),
@@ -511,8 +534,8 @@ def verify_cell(torch, device, args, seed: int):
             cell[mode] = {"median_us": r[mode]["median_us"],
                           "gb_per_s_distinct": round(nbytes / (r[mode]["median_us"] * 1e-6) / 1e9, 1)}
         cell["union_speedup_over_pairs"] = round(r["pairs"]["median_us"] / r["union"]["median_us"], 3)
-        res[f"tokens_{tokens}"] = cell
-        log(f"[verify {member} x{tokens}] {tokens * TOP_K} pairs, {distinct:.1f} distinct experts: "
+        res[f"tokens_{tokens}" + (f"_pool_{pool}" if pool else "")] = cell
+        log(f"[verify {member} x{tokens}{' pool ' + str(pool) if pool else ''}] {tokens * TOP_K} pairs, {distinct:.1f} distinct experts: "
             + "  ".join(f"{m} {r[m]['median_us']:.1f} us" for m in ("pairs", "floor", "sorted", "union")))
         del arms, V
         torch.cuda.empty_cache()
@@ -781,13 +804,15 @@ def main() -> int:
                 "per_launch_us": gu["decode"]["median_us"], "bytes_per_launch": gu["bytes_per_dispatch"],
                 # HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE passes over `--probe`,
                 # each calibrated on a plain copy of known size
-                "traffic": traffic, "traffic_source": traffic_file.name if traffic else None}
+                "traffic": traffic, "traffic_source": traffic_file.name if traffic else None,
+                "trace": "profiles/gemv_mfma_iq2_ks_routed_decode.md"}
     # every priced cell: its ratios and the reference's gates
     summary, gates = {}, {}
     for m, r in results.items():
         for c, cell in (r.get("cells") or {}).items():
             key = f"{m}_{c}" + (f"_x{r['tokens']}" if r.get("tokens", 1) != 1 else "")
-            summary[key] = {k: cell[k] for k in ("x_floor", "x_stream", "x_floor_grid") if k in cell}
+            summary[key] = {k: cell[k] for k in ("x_floor", "x_stream", "x_floor_grid", "within_bar_vs_grid_floor")
+                            if k in cell}
             summary[key].update(us=cell["decode"]["median_us"], floor_us=cell["floor"]["median_us"],
                                 gb_per_s=cell["decode"]["gb_per_s"])
             gates[key] = cell["gates"]
@@ -797,6 +822,9 @@ def main() -> int:
             summary[key] = {"x_floor": cell["x_floor"], "us": cell["decode"]["median_us"],
                             "floor_us": cell["floor"]["median_us"], "gb_per_s": cell["decode"]["gb_per_s"]}
             gates[key] = cell["gates"]
+    if "verify" in results:
+        summary["verify"] = {k: {m: v[m]["median_us"] for m in ("pairs", "sorted", "union")}
+                             for k, v in results["verify"].items() if k.startswith("tokens_")}
     if "prefill" in results:
         pf = results["prefill"]
         summary["prefill"] = {"producer_gb_per_s": pf["producer_gb_per_s"], "gemm_tflops": pf["gemm_tflops"],

@@ -68,6 +68,27 @@ struct TileScan {
     uint32_t group, mtile;
 };
 
+// The number of M-tiles of the work list (sum over groups of ceil(size / BM)),
+// by the same in-block scan as find_mtile; the same value in every thread.
+template <int BM, int THREADS = 256>
+__device__ __forceinline__ uint32_t count_mtiles(const uint32_t *offs, uint32_t n_groups, TileScan &ts) {
+    static_assert(THREADS >= 256, "the first 256 threads scan");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint32_t total = 0;
+    for (uint32_t base = 0; base < n_groups; base += 256) {
+        const uint32_t g = base + tid;
+        uint32_t cnt = 0;
+        if (tid < 256 && g < n_groups) cnt = (offs[g + 1] - offs[g] + BM - 1) / BM;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+        if (tid < 256 && lane == 0) ts.scan[wave] = cnt;
+        __syncthreads();
+        total += ts.scan[0] + ts.scan[1] + ts.scan[2] + ts.scan[3];
+        __syncthreads();  // the next round rewrites the totals
+    }
+    return total;
+}
+
 // The (group, M-tile) of work item t for a block of THREADS >= 256 threads
 // (the first 256 scan): group g of the
 // sorted slot ranges [offs[g], offs[g+1]) contributes ceil(size / BM)

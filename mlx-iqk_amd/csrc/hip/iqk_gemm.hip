@@ -5,19 +5,36 @@
 // vendored).  y[p] = x[row(p)] @ W[group(p)]^T for every slot p, fp16
 // operands, f32 accumulation, one fp16 rounding of each output.
 //
-// Work list.  Slots are sorted by group; a group of c slots needs ceil(c/BM)
-// M-tiles.  Block (t, n) finds the group owning M-tile t with an in-block scan
-// of the group sizes, so the launch needs no host-side knowledge of the
-// routing (no device->host sync) and no workspace; the grid is sized for the
-// worst case ceil(n_slots/BM) + n_groups M-tiles and surplus blocks exit.
+// The prefill's cost is streaming the fp16 weights (16 MiB per expert
+// projection, each read once per 64-slot M-tile), so the kernel is shaped
+// for HBM: every wavefront streams its own weight rows with the next step's
+// loads in flight, and the M-tiles of one expert run on one XCD, back to
+// back, so a weight block's second and later reads come from that XCD's L2.
 //
-// Tile.  256 threads, four wavefronts, BM x BN = 64 x 256; each wavefront
-// owns a 64 x 64 sub-tile as 4 x 4 v_mfma_f32_16x16x32_f16 tiles.  Any
-// out_features works: a lane's B row is its D column, so columns at or beyond
-// out_features are neither loaded nor stored, lane by lane.  With both
-// operands k-contiguous (x rows and W rows), an MFMA operand fragment is 16
-// contiguous bytes per lane, loaded straight from global memory and reused
-// four times from registers.
+// Work list.  Slots are sorted by group; a group of c slots needs ceil(c/BM)
+// M-tiles.  A first in-block scan of the group sizes counts the M-tiles T
+// (no host-side knowledge of the routing: no device->host sync, no
+// workspace); XCD x (blocks b with b % 8 == x) takes M-tiles
+// [x ceil(T/8), (x+1) ceil(T/8)) in order, each with all its column blocks
+// one after another, so the column blocks of a tile share its activations in
+// L2 and consecutive tiles of an expert share its weights.  A second scan
+// finds the tile's group.  The grid is sized for the worst case
+// ceil(n_slots/BM) + n_groups tiles; surplus blocks exit.
+//
+// Tile.  512 threads, eight wavefronts, BM x BN = 64 x 256; wavefront w owns
+// weight rows 32w .. 32w+31 of the block (the columns of
+// v_mfma_f32_32x32x16_f16) for both 32-slot row blocks.  Reduction steps of
+// 64: the step's activations (64 slots x 64 fp16) are staged in LDS, double
+// buffered, one barrier a step; each lane loads its weight row's four
+// 16-byte chunks of the step straight into registers (the four loads of a
+// row's 128 bytes are consecutive instructions, so the line is fetched
+// once).  Loads run three steps ahead of the MFMAs in four rotating register
+// sets (about 150 VGPRs: one block of eight wavefronts a CU), so a CU keeps
+// three steps of weights and activations, ~120 KB, in flight.  Any out_features works: a lane's B row is its D column,
+// so columns at or beyond out_features are neither loaded nor stored.  A
+// tile with at most 32 real slots skips its second row block's MFMAs.
+
+#include <type_traits>
 
 #include "iqk_device.h"
 #include "iqk_host.h"
@@ -25,9 +42,23 @@
 namespace iqk {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kGemmBM = 64;
-constexpr int kGemmBN = 256;
+constexpr int kGemmBM = 64;                   // slots per tile
+constexpr int kGemmWaves = 8;
+constexpr int kGemmThreads = 64 * kGemmWaves;
+constexpr int kGemmBN = 32 * kGemmWaves;      // weight rows (output columns) per block
+constexpr int kGemmBK = 64;                   // reduction elements per step
+constexpr int kGemmU = kGemmBK / 16;          // MFMAs (16-wide k chunks) per step and row block
+constexpr int kGemmAStride = 2 * kGemmBK + 16;  // LDS bytes per staged activation row
+constexpr int kGemmAChunks = kGemmBK / 8;     // 16-byte activation chunks per row and step
+constexpr int kGemmARows = kGemmThreads / kGemmAChunks;  // slot rows one staging pass covers
+constexpr int kGemmAPer = kGemmBM / kGemmARows;          // staging passes (16-byte chunks a thread moves a step)
+// Register sets per operand: loads run kGemmStages - 1 steps ahead.  On the
+// 2048-token Zipf prefill (gate [2048 x 4096]) two sets measured 1113 us,
+// four 987 us; eight sets, or four of 128-wide steps, spill at 256 VGPRs.
+constexpr int kGemmStages = 4;
+static_assert(kGemmBM % kGemmARows == 0 && kGemmThreads % kGemmAChunks == 0, "whole staging passes");
 
 struct GemmArgs {
     const uint16_t *x;
@@ -39,88 +70,181 @@ struct GemmArgs {
     uint32_t K, N, n_groups, n_slots, n_x_rows;
 };
 
-__device__ __forceinline__ half8_t load_frag(const uint16_t *p) {
-    return __builtin_bit_cast(half8_t, *reinterpret_cast<const uint4_t *>(p));
-}
-
-__global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs a) {
+// FULL: K is a multiple of kGemmStages 64-wide steps, so the step loop has
+// no branch at all: loads past the last step re-read it, stages past it are
+// never read.  Otherwise the last step may end past K (its upper half is
+// zeroed) and the step count is any.
+template <bool FULL>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void grouped_gemm_kernel(GemmArgs a) {
     __shared__ TileScan ts;
+    __shared__ __attribute__((aligned(16))) uint8_t as[2][kGemmBM * kGemmAStride];
+    // per slot of the tile: its output row, bit 31 set when its activations
+    // are real (else the row is NaN), or kNoStore
+    __shared__ uint32_t slot_dst[kGemmBM];
+    constexpr uint32_t kNoStore = 0x7fffffffu;  // above any row (n_slots <= 2^30)
+
     const int tid = threadIdx.x;
+    const uint32_t ncb = (a.N + kGemmBN - 1) / kGemmBN;  // column blocks
+    const uint32_t tiles = count_mtiles<kGemmBM, kGemmThreads>(a.offs, a.n_groups, ts);
+    const uint32_t per_xcd = (tiles + 7) / 8;
+    const uint32_t xcd = blockIdx.x & 7u, j = blockIdx.x >> 3;
+    if (j / ncb >= per_xcd) return;  // surplus block (uniform)
+    const uint32_t tile = xcd * per_xcd + j / ncb, cblock = j % ncb;
+    if (tile >= tiles) return;
     uint32_t g, mtile;
-    if (!find_mtile<kGemmBM>(a.offs, a.n_groups, blockIdx.x, ts, g, mtile)) return;  // surplus block
+    if (!find_mtile<kGemmBM, kGemmThreads>(a.offs, a.n_groups, tile, ts, g, mtile)) return;
 
     // Offsets and row indices are device data: a slot outside [0, n_slots)
     // is never stored, and a row outside x is never read (zero operand; the
     // slot's output row is NaN).
     const uint32_t gend = min(a.offs[g + 1], a.n_slots);
     const uint32_t m0 = a.offs[g] + mtile * kGemmBM;
-    const int wave = tid / 64, lane = tid % 64;
-    const int lr = lane % 16, lk = 8 * (lane / 16);
-    const uint32_t n0 = blockIdx.y * kGemmBN + wave * 64;
+    const uint32_t n0 = cblock * kGemmBN;
+    const uint32_t ksteps = (a.K + kGemmBK - 1) / kGemmBK;
 
-    const uint16_t *ap[4];
-    bool av[4];
+    // activation staging: thread t moves 16 bytes (chunk t % C) of slot rows
+    // t / C + R i a step (C chunks a row, R rows a pass, i < kGemmAPer)
+    const int arow = tid / kGemmAChunks, achunk = tid % kGemmAChunks;
+    // every load below is unconditional, from an in-bounds address (a dead
+    // row reads row 0, which exists: the entry point refuses an empty x), so
+    // the loads stay straight-line code and each wait is for exactly the step
+    // it needs
+    const uint16_t *asrc[kGemmAPer];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t p = m0 + 16 * i + lr;
-        const uint32_t xrow = p < gend ? a.xr[p] : a.n_x_rows;
-        av[i] = xrow < a.n_x_rows;
-        ap[i] = a.x + size_t(av[i] ? xrow : 0u) * a.K + lk;
-    }
-    const uint16_t *bp[4];
-    bool bv[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        bv[j] = n0 + 16 * j + lr < a.N;  // this lane's column
-        bp[j] = a.w + (size_t(g) * a.N + (bv[j] ? n0 + 16 * j + lr : 0u)) * a.K + lk;
-    }
-
-    float4_t acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-    const half8_t zero = {};
-    half8_t af[4], bf[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) af[i] = av[i] ? load_frag(ap[i]) : zero;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) bf[j] = bv[j] ? load_frag(bp[j]) : zero;
-    for (uint32_t k0 = 32; k0 <= a.K; k0 += 32) {
-        half8_t an[4], bn[4];
-        const bool more = k0 < a.K;
-        if (more) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) an[i] = av[i] ? load_frag(ap[i] + k0) : zero;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) bn[j] = bv[j] ? load_frag(bp[j] + k0) : zero;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        if (more) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) { af[i] = an[i]; bf[i] = bn[i]; }
+    for (int i = 0; i < kGemmAPer; ++i) {
+        const int row = arow + kGemmARows * i;
+        const uint32_t ap = m0 + uint32_t(row);
+        const uint32_t xrow = ap < gend ? a.xr[ap] : a.n_x_rows;
+        const bool alive = xrow < a.n_x_rows;
+        asrc[i] = a.x + size_t(alive ? xrow : 0u) * a.K + 8 * achunk;
+        if (achunk == 0) {  // one thread a slot: the epilogue's destination, read once
+            uint32_t dst = kNoStore;
+            if (ap < gend) {
+                const uint32_t yrow = a.yr ? a.yr[ap] : ap;
+                if (yrow < a.n_slots) dst = yrow | (alive ? 0x80000000u : 0u);
+            }
+            slot_dst[row] = dst;
         }
     }
+    // A dead slot's activations feed only its own output row, which is never
+    // stored (or stored as NaN), so they need no zeroing; elements past K
+    // would feed every row and are zeroed.
+    using AStage = uint4_t[kGemmAPer];
+    const auto load_a = [&](uint32_t s, AStage &v) {
+        s = min(s, ksteps - 1);
+#pragma unroll
+        for (int i = 0; i < kGemmAPer; ++i) {
+            uint32_t k = s * kGemmBK;
+            if constexpr (FULL) {
+                v[i] = load_u4(asrc[i] + k);
+            } else {
+                const bool live = k + 8 * achunk < a.K;
+                k = min(k, a.K - 8 * achunk - 8);
+                const uint4_t t = load_u4(asrc[i] + k);
+                v[i] = live ? t : uint4_t{0u, 0u, 0u, 0u};
+            }
+        }
+    };
+    const auto store_a = [&](int buf, const AStage &v) {
+#pragma unroll
+        for (int i = 0; i < kGemmAPer; ++i)
+            *reinterpret_cast<uint4_t *>(as[buf] + (arow + kGemmARows * i) * kGemmAStride + 16 * achunk) = v[i];
+    };
 
-    // D layout: lane holds rows 4*(lane/16) + r of column lane%16.
+    // this lane's weight row: column n0 + 32 wave + l % 32; chunk 2u + h of a
+    // step feeds MFMA u (lanes h = l / 32 hold its two k halves)
+    const int wave = tid >> 6, l = tid & 63, ln = l & 31, h = l >> 5;
+    const uint32_t col = n0 + 32 * wave + ln;
+    const bool bv = col < a.N;
+    const uint16_t *bsrc = a.w + (size_t(g) * a.N + (bv ? col : 0u)) * a.K + 8 * h;
+    // a column past out_features reads column 0 and is never stored (a D
+    // column depends on its own B column only), so it needs no zeroing
+    const auto load_b = [&](uint32_t s, uint4_t (&b)[kGemmU]) {
+        s = min(s, ksteps - 1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+        for (int u = 0; u < kGemmU; ++u) {
+            uint32_t k = s * kGemmBK + 16 * u;
+            if constexpr (!FULL) {
+                const bool live = k + 8 * h < a.K;
+                k = min(k, a.K - 8 * h - 8);
+                const uint4_t v = load_u4(bsrc + k);
+                b[u] = live ? v : uint4_t{0u, 0u, 0u, 0u};
+            } else {
+                b[u] = load_u4(bsrc + k);
+            }
+        }
+    };
+
+    // ST register sets per operand rotate through the steps: step s computes
+    // with B(s), issues the loads of step s + ST - 1 into the set step s - 1
+    // freed, and stages A(s + 1) into LDS before its barrier, so every load
+    // has ST - 1 steps to land and no set is copied.
+    uint4_t bq[kGemmStages][kGemmU];
+    AStage aq[kGemmStages];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t p = m0 + 16 * i + 4 * (lane / 16) + r;
-            if (p >= gend) continue;
-            const uint32_t yrow = a.yr ? a.yr[p] : p;
-            if (yrow >= a.n_slots) continue;
-            const bool real = a.xr[p] < a.n_x_rows;  // else the row is NaN
-            uint16_t *yp = a.y + size_t(yrow) * a.N + n0 + lr;  // only columns with bv[j] are stored
+    for (int i = 0; i + 1 < kGemmStages; ++i) {
+        load_a(i, aq[i]);
+        load_b(i, bq[i]);
+    }
+    store_a(0, aq[0]);
+    __syncthreads();  // the first activations and the slot table are in LDS
+
+    float16_t acc[2];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (bv[j]) yp[16 * j] = real ? uint16_t(float_to_half_bits(acc[i][j][r])) : kHalfNaN;
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[mb][r] = 0.f;
+
+    const auto run_steps = [&](auto slot_blocks) {
+        constexpr int MB = decltype(slot_blocks)::value;
+        // bc: B(s); bn: the set B(s + ST - 1) loads into; as1: A(s + 1),
+        // staged at the end of the step; an: the set A(s + ST - 1) loads into
+        const auto step = [&](uint32_t s, const uint4_t (&bc)[kGemmU], uint4_t (&bn)[kGemmU], const AStage &as1,
+                              AStage &an) {
+            load_a(s + kGemmStages - 1, an);
+            load_b(s + kGemmStages - 1, bn);
+            const uint8_t *ab = as[s & 1] + ln * kGemmAStride + 16 * h;
+#pragma unroll
+            for (int u = 0; u < kGemmU; ++u) {
+                const half8_t bf = __builtin_bit_cast(half8_t, bc[u]);
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    const half8_t af = __builtin_bit_cast(half8_t, *reinterpret_cast<const uint4_t *>(
+                                                                       ab + 32 * mb * kGemmAStride + 32 * u));
+                    acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc[mb], 0, 0, 0);
+                }
+            }
+            // the buffer every wavefront finished reading before the last
+            // barrier (after the last step: a stage nobody reads)
+            store_a((s + 1) & 1, as1);
+            __syncthreads();
+        };
+        for (uint32_t s = 0; s < ksteps; s += kGemmStages) {  // the step count and its bounds are uniform
+#pragma unroll
+            for (int i = 0; i < kGemmStages; ++i) {
+                if (FULL || s + i < ksteps)
+                    step(s + i, bq[i], bq[(i + kGemmStages - 1) % kGemmStages], aq[(i + 1) % kGemmStages],
+                         aq[(i + kGemmStages - 1) % kGemmStages]);
+            }
+        }
+    };
+    if (gend - m0 <= 32)  // uniform per block
+        run_steps(std::integral_constant<int, 1>{});
+    else
+        run_steps(std::integral_constant<int, 2>{});
+
+    // D layout (32x32): lane l, register r holds row 8(r/4) + 4(l/32) + r%4
+    // of column l % 32.
+    if (!bv) return;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t dst = slot_dst[32 * mb + 8 * (r >> 2) + 4 * h + (r & 3)];
+            if (dst != kNoStore)
+                a.y[size_t(dst & 0x7fffffffu) * a.N + col] =
+                    (dst >> 31) ? uint16_t(float_to_half_bits(acc[mb][r])) : kHalfNaN;
         }
     }
 }
@@ -137,7 +261,7 @@ extern "C" int iqk_grouped_gemm(int64_t in_features, int64_t out_features, int64
         return IQK_ERR_ARGUMENT;
     if (n_x_rows < 0 || n_x_rows > 0xffffffffll) return IQK_ERR_ARGUMENT;
     if (n_groups == 0 || n_slots == 0) return IQK_OK;
-    if (!x || !w || !group_offsets || !x_rows || !y) return IQK_ERR_ARGUMENT;
+    if (!x || !w || !group_offsets || !x_rows || !y || n_x_rows == 0) return IQK_ERR_ARGUMENT;
     GemmArgs a;
     a.x = static_cast<const uint16_t *>(x);
     a.w = static_cast<const uint16_t *>(w);
@@ -150,9 +274,13 @@ extern "C" int iqk_grouped_gemm(int64_t in_features, int64_t out_features, int64
     a.n_groups = uint32_t(n_groups);
     a.n_slots = uint32_t(n_slots);
     a.n_x_rows = uint32_t(n_x_rows);
+    // blocks: 8 XCDs x ceil(worst-case tiles / 8) x column blocks
     const uint64_t mtiles = (uint64_t(n_slots) + kGemmBM - 1) / kGemmBM + uint64_t(n_groups);
-    if (mtiles > 0x7fffffffull) return IQK_ERR_ARGUMENT;
-    const dim3 grid{uint32_t(mtiles), uint32_t((out_features + kGemmBN - 1) / kGemmBN)}, block{256};
-    hipLaunchKernelGGL(grouped_gemm_kernel, grid, block, 0, as_stream(stream), a);
+    const uint64_t blocks = 8 * ((mtiles + 7) / 8) * uint64_t((out_features + kGemmBN - 1) / kGemmBN);
+    if (blocks > 0x7fffffffull) return IQK_ERR_ARGUMENT;
+    if (in_features % (kGemmStages * kGemmBK) == 0)
+        hipLaunchKernelGGL(grouped_gemm_kernel<true>, dim3{uint32_t(blocks)}, dim3{kGemmThreads}, 0, as_stream(stream), a);
+    else
+        hipLaunchKernelGGL(grouped_gemm_kernel<false>, dim3{uint32_t(blocks)}, dim3{kGemmThreads}, 0, as_stream(stream), a);
     return record_launch(hipGetLastError());
 }

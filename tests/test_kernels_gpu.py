@@ -272,7 +272,44 @@ def test_floor_kernels_run(device, member, n):
 # -- the grouped GEMM -----------------------------------------------------------------
 
 
-@pytest.mark.parametrize("K,N", [(4096, 2048), (2048, 4096), (2048, 256), (2048, 32), (4096, 272)])
+def test_grouped_gemm_marks_rows_outside_x_with_nan(device):
+    """A slot whose activation row lies beyond x is never read: its output row
+    is NaN, every other row is unaffected; a y row beyond the slots is not
+    stored."""
+    rng = np.random.default_rng(5)
+    K, N, G = 2048, 96, 3
+    counts = np.array([40, 0, 30], dtype=np.int64)
+    P = int(counts.sum())
+    w = (rng.standard_normal((G, N, K)) * 0.02).astype(np.float16)
+    x = rng.standard_normal((50, K)).astype(np.float16)
+    x_rows = rng.integers(0, 50, size=P).astype(np.int32)
+    x_rows[[3, 45]] = [50, 2 ** 31 - 1]
+    offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    dev = {k: torch.from_numpy(v).to(device) for k, v in (("x", x), ("w", w), ("o", offs), ("r", x_rows))}
+    got = kernels.grouped_gemm(dev["x"], dev["w"], dev["o"], dev["r"]).float().cpu().numpy()
+    bad = np.zeros(P, dtype=bool)
+    bad[[3, 45]] = True
+    assert np.all(np.isnan(got[bad])) and not np.any(np.isnan(got[~bad]))
+    g_of = np.repeat(np.arange(G), counts)
+    want = np.stack([x[x_rows[p] % 50].astype(np.float64) @ w[g_of[p]].astype(np.float64).T for p in range(P)])
+    assert np.max(np.abs(got[~bad] - want[~bad])) / np.max(np.abs(want[~bad])) < 3e-3
+
+
+def test_grouped_gemm_is_deterministic(device):
+    rng = np.random.default_rng(7)
+    K, N = 4096, 512
+    counts = np.array([300, 3, 64, 65], dtype=np.int64)
+    P = int(counts.sum())
+    w = torch.from_numpy((rng.standard_normal((4, N, K)) * 0.02).astype(np.float16)).to(device)
+    x = torch.from_numpy(rng.standard_normal((P, K)).astype(np.float16)).to(device)
+    offs = torch.from_numpy(np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)).to(device)
+    rows = torch.arange(P, dtype=torch.int32, device=device)
+    a = kernels.grouped_gemm(x, w, offs, rows)
+    b = kernels.grouped_gemm(x, w, offs, rows)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("K,N", [(4096, 2048), (2048, 4096), (2048, 256), (2048, 32), (4096, 272), (2080, 96)])
 def test_grouped_gemm_matches_a_float64_reference(device, K, N):
     print(f"grouped gemm K={K} N={N}", flush=True)
     rng = np.random.default_rng(K + N)
