@@ -89,7 +89,8 @@ def parse() -> argparse.Namespace:
                          f"{PROBE_COPY_BYTES >> 20} MiB (the HBM-byte calibration), and exit")
     ap.add_argument("--probe-kernel", default="decode:iq2_ks:1:gate_up",
                     help="decode|floor|floor_grid:<member>:<tokens>:gate_up|down, or fused|producer|gemm:<member>:"
-                         "gate|down (the 2048-token Zipf prefill)")
+                         "gate|down (the 2048-token Zipf prefill), or pairs|sorted:<member>:<tokens>:<pool> (the "
+                         "verify shape: every token's top-6 from a pool of experts, gate geometry)")
     return ap.parse_args()
 
 
@@ -403,14 +404,16 @@ def prefill_cell(torch, device, args, seed: int):
         # each kernel timed over `burst` back-to-back dispatches (steady state, as
         # a prefill's projections run), rounds alternating the routes
         reps, burst = 3, 4
-        times = {"producer": [], "floor": [], "gemm": [], "fused": []}
+        times = {"producer": [], "floor": [], "gemm": [], "fused": [], "route": []}
         for _ in range(reps):
-            for key in ("producer", "floor", "gemm", "fused"):
+            for key in ("producer", "floor", "gemm", "fused", "route"):
                 a, b = ev(), ev()
                 a.record()
                 for _ in range(burst):
                     if key == "gemm":
                         kernels.grouped_gemm(xin.reshape(-1, n), w, offs, rows, out=yg)
+                    elif key == "route":
+                        kernels.route(ids, EXPERTS, 1, 1, flat.size)
                     elif key == "fused":
                         kernels.fused_matmul(member, xin.reshape(-1, n), mod._streams(), EXPERTS, out, offs_e, rows,
                                              out=yf)
@@ -450,7 +453,8 @@ def prefill_cell(torch, device, args, seed: int):
              "gemm_us": round(med["gemm"], 2), "gemm_flop": flop,
              "gemm_tflops": round(flop / (med["gemm"] * 1e-6) / 1e12, 2)}
         r["mfma_utilisation"] = round(r["gemm_tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
-        r.update({"module_forward_us": round(med["module"], 2), "module_forward_host_us": round(med["module_host"], 2),
+        r.update({"route_us": round(med["route"], 2),
+                  "module_forward_us": round(med["module"], 2), "module_forward_host_us": round(med["module_host"], 2),
                   "fused_us": round(med["fused"], 2), "fused_tflops": round(flop / (med["fused"] * 1e-6) / 1e12, 2),
                   "fused_speedup_over_producer_route": round((med["producer"] + med["gemm"]) / med["fused"], 2),
                   "fused_max_dev_vs_producer_route": round(fused_dev, 6)})
@@ -459,7 +463,7 @@ def prefill_cell(torch, device, args, seed: int):
         log(f"  {name}: producer {med['producer']:.1f} us ({r['producer_gb_per_s']} GB/s, x{r['producer_x_floor']})"
             f"  gemm {med['gemm']:.1f} us ({r['gemm_tflops']} TFLOP/s)"
             f"  fused {med['fused']:.1f} us ({r['fused_tflops']} TFLOP/s, dev {fused_dev:.2e})"
-            f"  module forward {med['module']:.1f} us GPU, {med['module_host']:.1f} us host")
+            f"  route {med['route']:.1f} us  module forward {med['module']:.1f} us GPU, {med['module_host']:.1f} us host")
         del mod, w, y, yf, yp
         torch.cuda.empty_cache()
         if name.startswith("gate_"):  # outside the prefill configuration's totals
@@ -724,7 +728,28 @@ def probe(torch, device, args) -> int:
 
     kind, member, *rest = args.probe_kernel.split(":")
     info = {"probe": args.probe, "kernel": args.probe_kernel}
-    if kind in ("decode", "floor", "floor_grid"):
+    if kind in ("pairs", "sorted"):
+        from mlx_iqk_amd import kernels, synth
+        tokens, pool = int(rest[0]), int(rest[1])
+        out, n = GU
+        stack = synth.expert_stack(member, EXPERTS, out, n, 31, device, args.distinct, "verify")
+        rng = np.random.default_rng(31)
+        distinct = []
+        for _ in range(args.probe):
+            src = rng.choice(EXPERTS, pool, replace=False)
+            idx = np.stack([rng.choice(src, TOP_K, replace=False) for _ in range(tokens)]).astype(np.int32)
+            flat = idx.reshape(-1)
+            order = np.argsort(flat, kind="stable")
+            x = torch.randn(tokens, n, device=device).to(torch.float16)
+            distinct.append(int(np.unique(flat).size))
+            if kind == "pairs":
+                kernels.gemv(member, x, stack, torch.from_numpy(flat).to(device), TOP_K, EXPERTS, out)
+            else:
+                kernels.gemv_sorted(member, x, stack, torch.from_numpy(flat[order]).to(device),
+                                    torch.from_numpy((order // TOP_K).astype(np.int32)).to(device), EXPERTS, out)
+        info["pair_bytes_per_dispatch"] = tokens * TOP_K * out * ik_row_bytes(member, n)
+        info["distinct_bytes_per_dispatch_mean"] = statistics.mean(distinct) * out * ik_row_bytes(member, n)
+    elif kind in ("decode", "floor", "floor_grid"):
         tokens, which = int(rest[0]), rest[1]
         gu_launch, dn_launch = decode_cell(torch, device, member, tokens, args, seed=11, launchers_only=True)
         launch = gu_launch if which == "gate_up" else dn_launch

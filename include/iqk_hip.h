@@ -109,15 +109,14 @@ int iqk_gemv_sorted(int member, int64_t in_features, int64_t out_features, int64
                     const uint32_t *sorted_ids, const uint32_t *toks, uint32_t mats,
                     void *y, void *stream);
 
-// The same contraction, one stream read per run of equal adjacent ids
+// The same contraction, one HBM read per run of equal adjacent ids
 // (replaces gemv_union_kernel + IqkSwitchLinear.gemv_union,
-// src/mlx_iqk/kernels.py:484-578, 834-853, src/mlx_iqk/nn.py:301-333): the
-// workgroup of a run's first pair computes every pair of the run from one
-// read of the expert's rows.  Arguments, output and refusals as
-// iqk_gemv_sorted, and bit-identical to it.  The run's pairs are computed one
-// after another, so with short runs (routing that rarely repeats an expert)
-// iqk_gemv_sorted is faster: its run's workgroups run side by side and share
-// the expert's bytes through L2.
+// src/mlx_iqk/kernels.py:484-578, 834-853, src/mlx_iqk/nn.py:301-333).
+// Arguments, output and refusals as iqk_gemv_sorted, and the same dispatch: a
+// run's pairs are adjacent workgroups, so HBM delivers the expert's rows once
+// and the run's other pairs read them from L2.  (The reference computes a
+// run's pairs one after another in one threadgroup; here that measured slower
+// on uniform and on pooled routing alike.)
 int iqk_gemv_union(int member, int64_t in_features, int64_t out_features, int64_t num_experts,
                    const void *x, int64_t n_x_rows, const void *const *streams, int n_streams,
                    const uint32_t *sorted_ids, const uint32_t *toks, uint32_t mats,
@@ -191,6 +190,24 @@ int iqk_fused_gemm(int member, int64_t in_features, int64_t out_features, int64_
                    int64_t row_start, int64_t rows, const uint32_t *group_offsets,
                    const uint32_t *x_rows, const uint32_t *y_rows, int64_t n_slots,
                    void *y, void *stream);
+
+// The prefill route's grouping of token-expert pairs into expert-sorted
+// slots, on the device, in one launch (replaces the pair sort the reference's
+// sorting caller performs, mlx_lm's _gather_sort, and the grouping inside
+// mx.gather_mm's sorted path, src/mlx_iqk/nn.py:221-238).  Pair p names
+// expert ids[p] (u32) and owns rows_per_pair slots; its activation rows are
+// (p / pairs_per_x_row) * rows_per_pair + r, its output rows p *
+// rows_per_pair + r (r < rows_per_pair).  Outputs, ready for iqk_fused_gemm
+// and iqk_grouped_gemm: group_offsets u32 [num_experts + 1] (slots of
+// experts < e; the last is n_pairs * rows_per_pair), and per slot x_rows and
+// y_rows u32 [n_pairs * rows_per_pair].  Slots are sorted by expert and keep
+// the pairs' order within an expert, so the lists are the same on every
+// call.  An id >= num_experts counts for expert 0 with x_rows = n_x_rows, so
+// the prefill kernels give its rows NaN and read nothing.  num_experts <=
+// 4096; n_x_rows must hold every activation row a pair names.
+int iqk_route(const uint32_t *ids, int64_t n_pairs, int64_t num_experts, int64_t rows_per_pair,
+              int64_t pairs_per_x_row, int64_t n_x_rows, uint32_t *group_offsets, uint32_t *x_rows,
+              uint32_t *y_rows, void *stream);
 
 // ik wire rows -> the member's relayout streams, on the GPU (replaces
 // format.pack for rows already in device memory, src/mlx_iqk/format.py:478-588,

@@ -329,17 +329,6 @@ struct LaneIq2ks {
         for (uint32_t s = 0; s < 4; ++s) q[s] = load_u4(bytes(a.s0) + (row * (N / 4) + 256 * kq + 64 * s + 16 * g));
     }
 
-    // The stream words as if reloaded: a loop over pairs then expands them
-    // anew each pair instead of keeping the expanded weights live.
-    __device__ __forceinline__ void launder() {
-        pin(sc);
-        pin(hb);
-        pin(ab);
-        pin(dvb);
-#pragma unroll
-        for (int s = 0; s < 4; ++s) pin(q[s]);
-    }
-
     __device__ __forceinline__ uint32_t hash() const {
         uint32_t h = 59u * (sc.x + sc.y + sc.z + sc.w) + 61u * hb + 71u * ab + 67u * dvb;
 #pragma unroll
@@ -445,16 +434,6 @@ struct LaneIq2k {
         dv = *reinterpret_cast<const uint2_t *>(bytes(a.s3) + (row * (N / 128) + 8 * kq));
 #pragma unroll
         for (uint32_t s = 0; s < 4; ++s) q[s] = load_u4(bytes(a.s0) + (row * (N / 4) + 256 * kq + 64 * s + 16 * g));
-    }
-
-    // The stream words as if reloaded (see LaneIq2ks::launder).
-    __device__ __forceinline__ void launder() {
-        pin(sc0);
-        pin(sc1);
-        pin(ex);
-        pin(dv);
-#pragma unroll
-        for (int s = 0; s < 4; ++s) pin(q[s]);
     }
 
     __device__ __forceinline__ uint32_t hash() const {
@@ -738,11 +717,13 @@ using LaneOf = std::conditional_t<MEMBER == IQ2_KS, LaneIq2ks<N>,
 enum GemvKind : int { kDecode = 0, kFloor = 1, kFloorGrid = 2 };
 
 // How a launch maps pairs to activation rows and stream reads.
+// Either way one workgroup serves one (row tile, pair).  Pairs sorted by
+// expert put a run's workgroups next to each other in the grid, so the run's
+// expert rows come from HBM once and from L2 for the run's other pairs: the
+// union form (the reference's one read per run) is this dispatch.
 enum GemvMode : int {
-    kPairs = 0,   // pair m reads x[m / pairs_per_row]; one workgroup per (tile, pair)
-    kSorted = 1,  // pair m reads x[toks[m]]; one workgroup per (tile, pair)
-    kUnion = 2,   // as kSorted, but a run of equal adjacent ids streams its
-                  // expert's rows once: the run's first pair does the run
+    kPairs = 0,   // pair m reads x[m / pairs_per_row]
+    kSorted = 1,  // pair m reads x[toks[m]]
 };
 
 // R = 1: six wavefronts per SIMD, three workgroups of eight (N = 4096) or
@@ -750,16 +731,14 @@ enum GemvMode : int {
 // workgroups are resident at once.  R = 2 (dispatches of many workgroups:
 // IQ1_S_R4, and the IQ2 members at 2048 wide): each wavefront takes 32 rows, two MFMA column blocks that
 // share every A read, so a workgroup stages its activations for 64 rows;
-// five wavefronts per SIMD.  kUnion re-expands a lane's stream words for
-// each pair of its run (the words are read once); five wavefronts per SIMD.
+// five wavefronts per SIMD.
 template <int MEMBER, int N, int FLOOR, int MODE, int R>
 __global__ __launch_bounds__((Gemv2Shape<MEMBER, N>::THREADS))
-__attribute__((amdgpu_waves_per_eu(MODE == kUnion || R == 2 ? 5 : 6)))
+__attribute__((amdgpu_waves_per_eu(R == 2 ? 5 : 6)))
 void gemv_mfma_kernel(Gemv2Args a) {
     using S = Gemv2Shape<MEMBER, N>;
     constexpr int KS = S::KS;
     constexpr int ROWS = kGroupRows * R;  // rows per workgroup
-    static_assert(MODE != kUnion || R == 1, "the union form keeps one row block per wavefront");
     __shared__ Gemv2Smem<MEMBER, N, R> sm;
 
     const int tid = threadIdx.x;
@@ -769,47 +748,16 @@ void gemv_mfma_kernel(Gemv2Args a) {
     const uint32_t m0 = MODE == kPairs ? blockIdx.z * a.pairs_per_row + blockIdx.y : blockIdx.z;
     const uint32_t rowg = blockIdx.x * ROWS;
 
-    // The run of pairs this workgroup serves: one pair, or for kUnion every
-    // pair of a run of equal ids (workgroups of the run's other pairs exit).
-    // The ids around m0 are read as one batch of independent loads (one
-    // latency, not a chain of them); a run longer than the batch reads on.
-    uint32_t run = 1;
-    if constexpr (MODE == kUnion) {
-        constexpr int kScan = 8;
-        uint32_t ids[kScan + 1];  // sel[m0 - 1 .. m0 + kScan - 1], where they exist
-#pragma unroll
-        for (int i = 0; i <= kScan; ++i) {
-            const uint32_t m = m0 + uint32_t(i) - 1u;
-            ids[i] = (i > 0 || m0 > 0) && m < a.mats ? a.sel[m] : 0u;
-        }
-        const uint32_t e_first = ids[1];
-        if (m0 > 0 && ids[0] == e_first) return;  // uniform: not the run's first pair
-        bool open = true;
-#pragma unroll
-        for (int i = 2; i <= kScan; ++i) {
-            open = open && m0 + uint32_t(i) - 1u < a.mats && ids[i] == e_first;
-            run += open ? 1u : 0u;
-        }
-        if (open)
-            while (m0 + run < a.mats && a.sel[m0 + run] == e_first) ++run;
-    }
-    // Activation row of pair m; a row beyond x reads row 0 and yields NaN.
-    const auto x_row = [&](uint32_t m) -> uint32_t {
-        return MODE == kPairs ? blockIdx.z : a.toks[m];
-    };
+    // Activation row of the pair; a row beyond x reads row 0 and yields NaN.
+    const uint32_t tok = MODE == kPairs ? blockIdx.z : a.toks[m0];
+    const bool x_ok = MODE == kPairs || tok < a.n_x_rows;
 
     // Activation (and IQ1_S_R4 grid) loads first: they do not wait for the
     // expert id, and vector loads retire in order, so staging them waits for
     // none of the stream bytes issued after them.
     const bool stager = tid < S::UNITS;  // uniform per wavefront
-    const auto load_x = [&](uint32_t tok, uint4_t &xv) {  // fp16 pairs 4tid .. 4tid+3 of row tok
-        xv = uint4_t{0u, 0u, 0u, 0u};
-        if (stager) xv = load_u4(bytes(a.x) + (tok * (2 * N) + 16 * uint32_t(tid)));
-    };
-    uint32_t tok = x_row(m0);
-    bool x_ok = MODE == kPairs || tok < a.n_x_rows;
-    uint4_t xv;
-    load_x(x_ok ? tok : 0u, xv);
+    uint4_t xv = {0u, 0u, 0u, 0u};         // fp16 pairs 4tid .. 4tid+3 of the pair's row
+    if (stager) xv = load_u4(bytes(a.x) + ((x_ok ? tok : 0u) * (2 * N) + 16 * uint32_t(tid)));
     constexpr bool IQ1 = MEMBER == IQ1_S_R4;
     // IQ1_S_R4: the codes of grid entries 4tid .. 4tid+3
     constexpr bool GRID = IQ1 && FLOOR != kFloor;
@@ -830,21 +778,8 @@ void gemv_mfma_kernel(Gemv2Args a) {
 #pragma unroll
     for (int r = 0; r < R; ++r) lane[r].load(a, e * a.out_features + rowg + 16 * (R * tile + r) + n, kq, g);
 
-    // One pair's contraction.  Outside kUnion it runs once, straight-line: a
-    // loop here, even of one trip, costs the pair kernels registers.
-    const auto contract = [&](uint32_t q) {
-        const uint32_t m = m0 + q;
-        if (q > 0) {  // kUnion: the run's next pair, same stream registers
-            tok = x_row(m);
-            x_ok = tok < a.n_x_rows;
-            load_x(x_ok ? tok : 0u, xv);
-            // expand them anew (not for the first pair: pinning a word still
-            // in flight would wait for every word up front)
-            if constexpr (MODE == kUnion) {
-#pragma unroll
-                for (int r = 0; r < R; ++r) lane[r].launder();
-            }
-        }
+    // The pair's contraction, straight-line code.
+    {
         float acc[R];
         if constexpr (FLOOR != kDecode) {
             uint32_t h = xv.x + 3u * xv.y + 5u * xv.z + 7u * xv.w;
@@ -863,7 +798,7 @@ void gemv_mfma_kernel(Gemv2Args a) {
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[r] = float((h >> r) & 0xffu);
         } else {
-            if (q == 0) {
+            {
                 if constexpr (GRID) {
                     uint4_t g0, g1;
                     expand_grid_pair(gridc.x, g0);
@@ -888,9 +823,9 @@ void gemv_mfma_kernel(Gemv2Args a) {
             const float *sbs = sm.sbs + (S::WK / 32) * kq;
             using Lane = LaneOf<MEMBER, N>;
             // the prologue of every super-block before the first code word,
-            // or (two row blocks, or a loop over a run's pairs) each just
-            // before its MFMAs: registers for a wavefront per SIMD
-            constexpr bool EARLY = R == 1 && MODE != kUnion;
+            // or (two row blocks) each just before its MFMAs: registers for a
+            // wavefront per SIMD
+            constexpr bool EARLY = R == 1;
             if constexpr (IQ1)
                 Lane::template decode<R, EARLY>(lane, abase, reads, sbs, sm.fsum + (S::WK / 32) * kq, sm.b8, g, acc);
             else if constexpr (MEMBER == IQ2_KS)
@@ -900,8 +835,7 @@ void gemv_mfma_kernel(Gemv2Args a) {
                                          sm.ktab, g, acc);
         }
         // Partials of the row's lanes and wavefronts: wave 0 sums them after
-        // the barrier; the next pair's staging and partials come only after
-        // its own barrier, which wave 0 reaches after summing.
+        // the barrier.
 #pragma unroll
         for (int r = 0; r < R; ++r) sm.part[kq][g][16 * (R * tile + r) + n] = acc[r];
         __syncthreads();
@@ -910,15 +844,8 @@ void gemv_mfma_kernel(Gemv2Args a) {
 #pragma unroll
             for (int k = 0; k < KS; ++k)
                 sum += (sm.part[k][0][tid] + sm.part[k][1][tid]) + (sm.part[k][2][tid] + sm.part[k][3][tid]);
-            a.y[size_t(m) * a.out_features + rowg + tid] = valid && x_ok ? uint16_t(float_to_half_bits(sum)) : kHalfNaN;
+            a.y[size_t(m0) * a.out_features + rowg + tid] = valid && x_ok ? uint16_t(float_to_half_bits(sum)) : kHalfNaN;
         }
-    };
-    // The run's first pair is straight-line code, as in the other forms, so
-    // its staging waits for the activations only, not for the stream words
-    // (inside a loop the compiler waits for every load first).
-    contract(0);
-    if constexpr (MODE == kUnion) {
-        for (uint32_t q = 1; q < run; ++q) contract(q);
     }
 }
 
@@ -958,12 +885,11 @@ constexpr uint64_t kTwoRowMinGroupsIq2 = 8 * 768;
 // Called by the GEMV entry points (after their argument checks) when
 // out_features is a multiple of the workgroup's 32 rows; returns -1 when this
 // path does not apply.  `toks` NULL = pairs mode (x row m / pairs_per_row);
-// else x row toks[m] of n_x_rows, and `union_runs` selects the one-read-per-
-// run form.
+// else x row toks[m] of n_x_rows (the sorted and union entry points, one
+// dispatch: see GemvMode).
 int gemv_mfma_dispatch(int floor, int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
                        int64_t n_x_rows, const void *const *streams, int n_streams, const uint32_t *sel,
-                       const uint32_t *toks, bool union_runs, uint32_t pairs_per_row, uint32_t mats, void *y,
-                       hipStream_t st) {
+                       const uint32_t *toks, uint32_t pairs_per_row, uint32_t mats, void *y, hipStream_t st) {
     if (out % kGroupRows) return -1;
     // 32-bit offsets: every stream (the code plane is the largest, N/4 bytes a
     // row) and the activations stay below 4 GiB
@@ -1004,8 +930,7 @@ int gemv_mfma_dispatch(int floor, int member, int64_t n, int64_t out, int64_t nu
         }
     }
     if (floor != kDecode) return IQK_ERR_ARGUMENT;
-    return union_runs ? launch_member<kDecode, kUnion, 1>(member, n, a, mats, st)
-                      : launch_member<kDecode, kSorted, 1>(member, n, a, mats, st);
+    return launch_member<kDecode, kSorted, 1>(member, n, a, mats, st);
 }
 
 }  // namespace iqk

@@ -50,6 +50,8 @@ SIGNATURES = {
                                   c_void_p, c_int64, c_void_p, c_void_p]),
     "iqk_grouped_gemm": (c_int, [c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p,
                                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "iqk_route": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
+                          c_void_p]),
     "iqk_pack": (c_int, [c_int, c_int64, c_int64, c_void_p, ctypes.POINTER(c_void_p), c_int, c_void_p]),
     "iqk_fused_gemm": (c_int, [c_int, c_int64, c_int64, c_int64, c_void_p, c_int64, ctypes.POINTER(c_void_p),
                                c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),

@@ -38,6 +38,7 @@ HIP_SOURCES = {
     "iqk_fused_gemm.hip": (),
     "iqk_pack.hip": (),
     "iqk_floor.hip": (),
+    "iqk_route.hip": (),
 }
 OFFLOAD_ARCH = "gfx950"
 

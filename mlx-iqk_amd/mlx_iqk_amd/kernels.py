@@ -187,10 +187,11 @@ def gemv_sorted(member: str, x: torch.Tensor, streams: list[torch.Tensor], sorte
     """Decode GEMV over expert-sorted pairs: ``y[p] = W[sorted_ids[p]] @ x[toks[p]]``.
 
     fp16 ``[mats, out]``; each element equals :func:`gemv`'s for the same
-    (expert, activation row), bit for bit.  ``union=True`` streams each run of
-    equal adjacent ids once (the multi-token verify shape,
-    src/mlx_iqk/kernels.py:484-578); otherwise one workgroup per pair
-    (src/mlx_iqk/kernels.py:404-482).  IQ2 members only.
+    (expert, activation row), bit for bit.  ``union=True`` is the union entry
+    point (the multi-token verify shape, src/mlx_iqk/kernels.py:484-578),
+    otherwise the sorted one (src/mlx_iqk/kernels.py:404-482); both run one
+    workgroup per pair, a run's adjacent workgroups sharing its expert's rows
+    through L2.  IQ2 members only.
     """
     check_iq2_member(member)
     n = int(x.shape[-1])
@@ -351,6 +352,41 @@ def pack(member: str, wire: torch.Tensor, in_features: int,
     return out
 
 
+ROUTE_MAX_EXPERTS = 4096
+"""Stacks the device-side route serves (its counters live in LDS)."""
+
+
+def route(ids: torch.Tensor, num_experts: int, rows_per_pair: int = 1, pairs_per_x_row: int = 1,
+          n_x_rows: int | None = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Expert-sorted slots of token-expert pairs, on the device, one launch.
+
+    ``ids`` int32/uint32 ``[P]``: pair p's expert (an id outside
+    ``[0, num_experts)``, read as u32, is grouped with expert 0 and given no
+    activation row, so the prefill kernels answer it with NaN rows).  Pair p
+    owns ``rows_per_pair`` slots whose activation rows are
+    ``(p // pairs_per_x_row) * rows_per_pair + r`` and output rows
+    ``p * rows_per_pair + r``.  Returns int32 ``group_offsets [E + 1]``,
+    ``x_rows [P * rows_per_pair]``, ``y_rows [P * rows_per_pair]``; the slot
+    order is stable (pairs keep their order within an expert).
+    """
+    _require_cuda(ids, "ids", (torch.int32, torch.uint32))
+    if ids.dim() != 1:
+        raise IqkKernelError("ids must be [pairs]")
+    E, P, M, ppx = int(num_experts), int(ids.numel()), int(rows_per_pair), int(pairs_per_x_row)
+    if not 0 < E <= ROUTE_MAX_EXPERTS:
+        raise IqkKernelError(f"the device route serves 1 .. {ROUTE_MAX_EXPERTS} experts, got {E}")
+    if M <= 0 or ppx <= 0:
+        raise IqkKernelError("rows_per_pair and pairs_per_x_row must be positive")
+    rows = ((P + ppx - 1) // ppx) * M if n_x_rows is None else int(n_x_rows)
+    offs = torch.empty(E + 1, dtype=torch.int32, device=ids.device)
+    x_rows = torch.empty(P * M, dtype=torch.int32, device=ids.device)
+    y_rows = torch.empty(P * M, dtype=torch.int32, device=ids.device)
+    rc = _native.load().iqk_route(ids.data_ptr(), P, E, M, ppx, rows, offs.data_ptr(), x_rows.data_ptr(),
+                                  y_rows.data_ptr(), _stream_ptr(ids.device))
+    _native.check(rc, f"iqk_route(P={P}, E={E}, M={M})")
+    return offs, x_rows, y_rows
+
+
 FUSED_MEMBERS = MEMBERS
 """Members the fused prefill contraction covers (all three)."""
 
@@ -399,6 +435,6 @@ __all__ = [
     "DEQUANT_THREADS", "IQ2_MEMBERS", "MEMBERS", "ROWS_PER_TG",
     "SUPPORTED_IN_FEATURES", "TABLE_INPUT_NAMES", "WEIGHTS_PER_LANE", "IqkKernelError",
     "check_dequant_geometry", "check_gemv_geometry", "check_streams", "dequant", "dequant_input_names",
-    "FUSED_MEMBERS", "check_iq2_member", "fused_matmul", "gemv", "pack", "stream_floor", "gemv_input_names", "gemv_sorted", "grouped_gemm",
+    "FUSED_MEMBERS", "ROUTE_MAX_EXPERTS", "check_iq2_member", "fused_matmul", "gemv", "pack", "route", "stream_floor", "gemv_input_names", "gemv_sorted", "grouped_gemm",
     "stream_dtypes",
 ]

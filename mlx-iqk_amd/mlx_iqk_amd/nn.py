@@ -217,13 +217,13 @@ class IqkSwitchLinear(torch.nn.Module):
                                    self.out_features)
 
     def gemv_union(self, x: torch.Tensor, sorted_ids: torch.Tensor, toks: torch.Tensor) -> torch.Tensor:
-        """:meth:`gemv_sorted` reading each distinct expert once per run of
-        equal adjacent ids: the multi-token verify shape, where several pairs
-        select one expert (reference: src/mlx_iqk/nn.py:301-333).  Output and
-        arithmetic identical to :meth:`gemv_sorted`; the caller applies the
-        inverse permutation.  A run's pairs are computed one after another,
-        so for routing that rarely repeats an expert :meth:`gemv_sorted` is
-        the faster of the two."""
+        """:meth:`gemv_sorted` reading each distinct expert from HBM once per
+        run of equal adjacent ids: the multi-token verify shape, where several
+        pairs select one expert (reference: src/mlx_iqk/nn.py:301-333).  Output
+        and arithmetic identical to :meth:`gemv_sorted`, and the same
+        dispatch: a run's pairs are adjacent workgroups that share the
+        expert's rows through L2.  The caller applies the inverse
+        permutation."""
         xt, sel, tok = self._sorted_operands(x, sorted_ids, toks)
         return kernels.gemv_sorted(self.member, xt, self._streams(), sel, tok, self.num_experts,
                                    self.out_features, union=True)
@@ -275,45 +275,61 @@ class IqkSwitchLinear(torch.nn.Module):
         P = math.prod(batch)
         if P == 0:
             return torch.empty(tuple(batch) + (M, rows), dtype=torch.float16, device=device)
-        xbatch = tuple(xb.shape[:-2])
         xflat = xb.reshape(-1, self.in_features).contiguous()
+        E = self.num_experts
+        offsets, x_rows, y_rows = self._route(tuple(xb.shape[:-2]), batch, indices, M, xflat.shape[0])
+        if self.fused_prefill and self.member in kernels.FUSED_MEMBERS:
+            y = kernels.fused_matmul(self.member, xflat, self._streams(), E, self.out_features, offsets, x_rows,
+                                     y_rows, row_start=start, rows=rows)
+            return y.reshape(tuple(batch) + (M, rows))
+        # The producer route: experts are routed only if some pair names them;
+        # compact them into slots in expert order (n_slots is an upper bound
+        # known on the host) and carry the group offsets over to the slots.
+        n_slots = min(E, P)
+        present = offsets[1:] > offsets[:-1]
+        slot_of_expert = torch.where(present, torch.cumsum(present, 0, dtype=torch.int32) - 1,
+                                     torch.full_like(offsets[1:], -1))
+        slot_offsets = torch.full((n_slots + 2,), P * M, dtype=torch.int32, device=device)
+        slot_offsets.scatter_(0, torch.where(present, slot_of_expert, n_slots + 1).to(torch.int64), offsets[:-1])
+        slot_offsets = slot_offsets[:n_slots + 1].contiguous()
+        w = kernels.dequant(self.member, self._streams(), E, self.out_features, self.in_features,
+                            slot_of_expert=slot_of_expert, n_slots=n_slots, row_start=start, rows=rows)
+        y = kernels.grouped_gemm(xflat, w, slot_offsets, x_rows, y_rows)
+        return y.reshape(tuple(batch) + (M, rows))
+
+    def _route(self, xbatch: tuple, batch: tuple, indices: torch.Tensor, M: int, n_x_rows: int):
+        """Group offsets (per expert, in slots) and each slot's activation and
+        output row, slots sorted by expert.  An id outside [0, E) reaches no
+        index op (ROCm builds drop torch's device-side bounds asserts): its
+        pair is grouped with expert 0 and given an activation row beyond x,
+        which the kernels never read and answer with a NaN output row -- what
+        the decode route returns."""
+        device = self.qs.device
+        E = self.num_experts
+        # pairs per activation row when x broadcasts over trailing batch dims
+        # only (gate/up: x [T, 1, 1, in] with indices [T, k]; sorted pairs:
+        # x [P, 1, in] with indices [P]): then one device launch does it all
+        pad = (1,) * (len(batch) - len(xbatch)) + tuple(xbatch)
+        lead = 0
+        while lead < len(batch) and pad[lead] == batch[lead]:
+            lead += 1
+        if all(d == 1 for d in pad[lead:]) and E <= kernels.ROUTE_MAX_EXPERTS:
+            ids = self._device_ids(indices.to(device).broadcast_to(batch))
+            return kernels.route(ids, E, M, math.prod(batch[lead:]), n_x_rows)
         xidx = torch.arange(math.prod(xbatch), device=device).reshape(xbatch).broadcast_to(batch).reshape(-1)
         raw = indices.to(device=device, dtype=torch.int64).broadcast_to(batch).reshape(-1)
-        E = self.num_experts
-        # An id outside [0, E) must reach no index op below (ROCm builds drop
-        # torch's device-side bounds asserts): its pair is grouped with expert
-        # 0 and given an activation row beyond x, which the kernels never read
-        # and answer with a NaN output row -- what the decode route returns.
         valid = (raw >= 0) & (raw < E)
         ids = torch.where(valid, raw, torch.zeros_like(raw))
         order = torch.argsort(ids, stable=True)
         r = torch.arange(M, device=device)
-        no_row = torch.full_like(xidx, xflat.shape[0])
+        no_row = torch.full_like(xidx, n_x_rows)
         x_rows = (torch.where(valid, xidx, no_row)[order][:, None] * M + r).reshape(-1)
-        x_rows = torch.clamp(x_rows, max=xflat.shape[0]).to(torch.int32)
+        x_rows = torch.clamp(x_rows, max=n_x_rows).to(torch.int32)
         y_rows = (order[:, None] * M + r).reshape(-1).to(torch.int32)
-        if self.fused_prefill and self.member in kernels.FUSED_MEMBERS:
-            counts = torch.zeros(E, dtype=torch.int64, device=device).index_add_(0, ids, torch.full_like(ids, M))
-            offsets = torch.zeros(E + 1, dtype=torch.int32, device=device)
-            offsets[1:] = torch.cumsum(counts, 0).to(torch.int32)
-            y = kernels.fused_matmul(self.member, xflat, self._streams(), E, self.out_features, offsets, x_rows,
-                                     y_rows, row_start=start, rows=rows)
-            return y.reshape(tuple(batch) + (M, rows))
-        # Experts are routed only if some pair names them; compact them into
-        # slots in expert order.  n_slots is an upper bound known on the host.
-        present = torch.zeros(E, dtype=torch.int32, device=device).index_fill_(0, ids, 1)
-        slot_of_expert = torch.where(present > 0, torch.cumsum(present, 0, dtype=torch.int32) - 1,
-                                     torch.full_like(present, -1))
-        n_slots = min(E, P)
-        slot_of_pair = slot_of_expert[ids].to(torch.int64)
-        counts = torch.zeros(n_slots, dtype=torch.int64, device=device).index_add_(
-            0, slot_of_pair, torch.full_like(slot_of_pair, M))
-        offsets = torch.zeros(n_slots + 1, dtype=torch.int32, device=device)
+        counts = torch.zeros(E, dtype=torch.int64, device=device).index_add_(0, ids, torch.full_like(ids, M))
+        offsets = torch.zeros(E + 1, dtype=torch.int32, device=device)
         offsets[1:] = torch.cumsum(counts, 0).to(torch.int32)
-        w = kernels.dequant(self.member, self._streams(), E, self.out_features, self.in_features,
-                            slot_of_expert=slot_of_expert, n_slots=n_slots, row_start=start, rows=rows)
-        y = kernels.grouped_gemm(xflat, w, offsets, x_rows, y_rows)
-        return y.reshape(tuple(batch) + (M, rows))
+        return offsets, x_rows, y_rows
 
 
 __all__ = ["DECODE_MAT_LIMIT", "IqkKernelError", "IqkRuntimeError", "IqkSwitchLinear", "grid_table",

@@ -142,6 +142,20 @@ def test_fused_gemm_refuses_bad_arguments(lib):
     assert f(1, 4096, 2048, 8, p, 4, streams, 4, 0, 2048, p, p, None, 0, p, None) == _native.OK
 
 
+def test_route_refuses_bad_arguments(lib):
+    p = ctypes.c_void_p(16)  # never dereferenced: every call below is refused first
+    f = lib.iqk_route
+    assert f(p, 8, 0, 1, 1, 8, p, p, p, None) == _native.ERR_ARGUMENT       # no experts
+    assert f(p, 8, 4097, 1, 1, 8, p, p, p, None) == _native.ERR_ARGUMENT    # past the LDS counters
+    assert f(p, -1, 8, 1, 1, 8, p, p, p, None) == _native.ERR_ARGUMENT
+    assert f(p, 8, 8, 0, 1, 8, p, p, p, None) == _native.ERR_ARGUMENT       # rows per pair
+    assert f(p, 8, 8, 1, 0, 8, p, p, p, None) == _native.ERR_ARGUMENT       # pairs per x row
+    assert f(p, 8, 8, 2, 4, 3, p, p, p, None) == _native.ERR_ARGUMENT       # x holds 4 of the 2 x 2 rows named
+    assert f(None, 8, 8, 1, 1, 8, p, p, p, None) == _native.ERR_ARGUMENT
+    assert f(p, 8, 8, 1, 1, 8, None, p, p, None) == _native.ERR_ARGUMENT
+    assert f(p, 1 << 30, 8, 2, 1, 1 << 31, p, p, p, None) == _native.ERR_ARGUMENT  # 2^31 slots
+
+
 def test_pack_refuses_bad_arguments(lib):
     p = ctypes.c_void_p(16)  # never dereferenced: every call below is refused first
     streams = _native.pointer_array([16] * 5)

@@ -317,9 +317,9 @@ def test_union_gemv_covers_the_run_extremes(device, member):
 
 @pytest.mark.parametrize("member", IQ2)
 def test_union_runs_past_the_id_batch_and_invalid_ids(device, member):
-    """Runs longer than the kernel's batch of eight ids, one ending on it, and
-    ids beyond the stack (0xFFFFFFFF first, the stack size last): the union
-    form equals the sorted form bit for bit, and invalid ids give NaN rows."""
+    """Runs of 1 to 10 pairs and ids beyond the stack (0xFFFFFFFF first, the
+    stack size last): the union form equals the sorted form bit for bit, and
+    invalid ids give NaN rows."""
     n = 2048
     module, _ = _module(member, n, 97, device)
     runs = [(0xFFFFFFFF, 1), (0, 10), (1, 1), (2, 7), (3, 8), (1, 3), (EXPERTS, 3)]
