@@ -7,34 +7,34 @@
 // whose outputs are exactly what the prefill kernels take: group offsets in
 // slots, and each slot's activation row and output row.
 //
-// One workgroup of 1024 threads, everything in LDS (no workspace).  A pass
-// loads 16 ids a thread at once (16384 pairs: one memory latency), kept in
-// registers for both phases, and takes them 1024 at a time (a batch);
-// within a wavefront the lanes holding one expert
-// id find each other by ballots over the id bits (an id >= num_experts counts
-// for expert 0: its slots keep an activation row past x, so the prefill
-// kernels answer them with NaN rows and read nothing), and the lowest such
-// lane speaks for all of them.
-//   1. histogram: one LDS atomic per (wavefront, expert) of a batch;
-//   2. an exclusive scan of the counts -> group offsets and per-expert cursors;
-//   3. a stable scatter: each wavefront posts its per-expert counts of the
-//      batch in a byte table, a pair's slot is its expert's cursor + the
-//      counts of the wavefronts before it + its rank among its wavefront's
-//      lanes, and the cursors then advance by the batch's counts.  Pairs keep
-//      their order within an expert, so the slot lists are the same on every
-//      call; three barriers a batch.
+// A pair's key is its expert id; an id >= num_experts keys as expert 0 (its
+// slots keep an activation row past x, so the prefill kernels answer them with
+// NaN rows and read nothing).  Expert e's slots are
+//   [#{pairs keyed below e}, #{pairs keyed below e + 1}),
+// its pairs in pair order (a stable counting sort).
+//
+// One workgroup per expert, so a launch spreads over the chip; no workspace.
+// Its eight wavefronts each take a contiguous eighth of the pairs and hold
+// their ids in registers (re-read from L2 only past 2048 pairs a wavefront):
+//   1. each wavefront counts, by ballots, its pairs keyed below e and keyed e;
+//   2. the eight totals through LDS give the group offset and each
+//      wavefront's first slot (the offset + the e-pairs of the wavefronts
+//      before it);
+//   3. each wavefront with e-pairs writes them in order, a pair's slot being
+//      its wavefront's next slot + its rank among the ballot's lanes.
+// Every block reads the whole id list (4 bytes a pair from L2); the time is
+// the two ballot passes over one wavefront's share, about P / 512 steps.
 
 #include "iqk_device.h"
 #include "iqk_host.h"
 
 namespace iqk {
 
-constexpr int kRouteThreads = 1024;
+constexpr int kRouteThreads = 512;
 constexpr int kRouteWaves = kRouteThreads / 64;
-constexpr int kRouteMaxExperts = 4096;        // LDS counters; 12 id bits
-constexpr int kRouteIdBits = 12;
-constexpr int kRoutePer = 16;                  // ids a thread holds
-constexpr uint32_t kRouteSpan = kRoutePer * kRouteThreads;  // pairs a pass holds
+constexpr int kRouteMaxExperts = 4096;
+constexpr int kRoutePer = 32;  // ids a lane holds per round
+constexpr uint32_t kRouteRound = 64u * kRoutePer;  // pairs a wavefront holds
 
 struct RouteArgs {
     const uint32_t *ids;
@@ -44,114 +44,70 @@ struct RouteArgs {
     uint32_t P, E, M, ppx, n_x_rows;
 };
 
-// The lanes of this wavefront that hold e (among the `live` ones).
-__device__ __forceinline__ uint64_t same_lanes(uint32_t e, bool live) {
-    uint64_t same = __ballot(live);
-#pragma unroll
-    for (int b = 0; b < kRouteIdBits; ++b) {
-        const uint64_t ones = __ballot((e >> b) & 1u);
-        same &= ((e >> b) & 1u) ? ones : ~ones;
-    }
-    return same;
-}
-
 __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a) {
-    __shared__ uint32_t cur[kRouteMaxExperts];
-    __shared__ uint8_t wcnt[kRouteWaves][kRouteMaxExperts];  // a batch's counts per wavefront (<= 64)
-    __shared__ uint32_t wtot[kRouteWaves];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ uint32_t tot[2][kRouteWaves];  // per wavefront: pairs keyed below e, keyed e
+    const uint32_t e = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint64_t below = (uint64_t(1) << lane) - 1u;
+    // wavefront w takes pairs [lo, hi): contiguous, in wavefront order
+    const uint32_t share = (a.P + 64u * kRouteWaves - 1u) / (64u * kRouteWaves) * 64u;
+    const uint32_t lo = min(a.P, uint32_t(wave) * share), hi = min(a.P, lo + share);
 
-    for (uint32_t e = tid; e < a.E; e += kRouteThreads) {
-        cur[e] = 0;
+    // raw ids of pairs base + 64 i + lane; lanes past hi load pair hi - 1 and
+    // are masked by `live` (only called with lo <= base < hi)
+    uint32_t raw[kRoutePer];
+    const auto load = [&](uint32_t base) {
 #pragma unroll
-        for (int w = 0; w < kRouteWaves; ++w) wcnt[w][e] = 0;
-    }
-    // ids of pairs span + 1024 i + tid, i < kRoutePer (past P: none)
-    uint32_t id[kRoutePer];
-    const auto load_span = [&](uint32_t span) {
-#pragma unroll
-        for (int i = 0; i < kRoutePer; ++i) {
-            const uint32_t p = span + uint32_t(kRouteThreads * i + tid);
-            id[i] = p < a.P ? a.ids[p] : 0u;
-        }
+        for (int i = 0; i < kRoutePer; ++i) raw[i] = a.ids[min(base + uint32_t(64 * i + lane), hi - 1u)];
     };
-    __syncthreads();
-    for (uint32_t span = 0; span < a.P; span += kRouteSpan) {
-        load_span(span);
+
+    uint32_t lt = 0, eq = 0;
+    for (uint32_t base = lo; base < hi; base += kRouteRound) {
+        load(base);
 #pragma unroll
         for (int i = 0; i < kRoutePer; ++i) {
-            const uint32_t p = span + uint32_t(kRouteThreads * i + tid);
-            const bool live = p < a.P;
-            const uint32_t e = id[i] < a.E ? id[i] : 0u;
-            const uint64_t same = same_lanes(e, live);
-            if (live && (same & below) == 0) atomicAdd(&cur[e], uint32_t(__popcll(same)));
+            const bool live = base + uint32_t(64 * i + lane) < hi;
+            const uint32_t key = raw[i] < a.E ? raw[i] : 0u;
+            lt += uint32_t(__popcll(__ballot(live && key < e)));
+            eq += uint32_t(__popcll(__ballot(live && key == e)));
         }
     }
+    if (lane == 0) {
+        tot[0][wave] = lt;
+        tot[1][wave] = eq;
+    }
     __syncthreads();
+    uint32_t first = 0, slot = 0;
+#pragma unroll
+    for (int w = 0; w < kRouteWaves; ++w) {
+        first += tot[0][w];
+        if (w < wave) slot += tot[1][w];
+    }
+    slot += first;
+    if (threadIdx.x == 0) {
+        a.offs[e] = first * a.M;
+        if (e == a.E - 1u) a.offs[a.E] = a.P * a.M;
+    }
+    if (eq == 0) return;  // uniform: no e-pairs in this wavefront's share
 
-    // exclusive scan: thread t owns experts 4t .. 4t+3
-    uint32_t c[4], sum = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t e = 4 * uint32_t(tid) + i;
-        c[i] = e < a.E ? cur[e] : 0u;
-        sum += c[i];
-    }
-    uint32_t incl = sum;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t up = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += up;
-    }
-    if (lane == 63) wtot[wave] = incl;
-    __syncthreads();
-    uint32_t before = incl - sum;
-    for (int w = 0; w < wave; ++w) before += wtot[w];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t e = 4 * uint32_t(tid) + i;
-        if (e < a.E) {
-            cur[e] = before;
-            a.offs[e] = before * a.M;
-        }
-        before += c[i];
-    }
-    if (tid == 0) a.offs[a.E] = a.P * a.M;
-    __syncthreads();
-
-    for (uint32_t span = 0; span < a.P; span += kRouteSpan) {
-        if (a.P > kRouteSpan) load_span(span);  // one span: the ids are still held
+    for (uint32_t base = lo; base < hi; base += kRouteRound) {
+        if (hi - lo > kRouteRound) load(base);  // one round: the ids are still held
 #pragma unroll
         for (int i = 0; i < kRoutePer; ++i) {
-            if (span + uint32_t(kRouteThreads * i) >= a.P) break;  // uniform
-            const uint32_t p = span + uint32_t(kRouteThreads * i + tid);
-            const bool live = p < a.P;
-            const bool valid = id[i] < a.E;
-            const uint32_t e = valid ? id[i] : 0u;
-            const uint64_t same = same_lanes(e, live);
-            const uint32_t rank = __popcll(same & below);
-            const bool leader = live && rank == 0;
-            if (leader) wcnt[wave][e] = uint8_t(__popcll(same));
-            __syncthreads();
-            uint32_t slot = 0;
-            if (live) {
-                slot = cur[e] + rank;
-                for (int w = 0; w < wave; ++w) slot += wcnt[w][e];
-            }
-            __syncthreads();  // every cursor and count read before any changes
-            if (leader) {
-                atomicAdd(&cur[e], uint32_t(__popcll(same)));
-                wcnt[wave][e] = 0;
-            }
-            if (live) {
+            const uint32_t p = base + uint32_t(64 * i + lane);
+            const bool valid = raw[i] < a.E;
+            const bool mine = p < hi && (valid ? raw[i] : 0u) == e;
+            const uint64_t m = __ballot(mine);
+            if (m == 0) continue;  // uniform
+            if (mine) {
+                const uint32_t s = (slot + uint32_t(__popcll(m & below))) * a.M;
                 const uint32_t xrow = valid ? (p / a.ppx) * a.M : a.n_x_rows;
                 for (uint32_t r = 0; r < a.M; ++r) {
-                    a.yr[slot * a.M + r] = p * a.M + r;
-                    a.xr[slot * a.M + r] = valid ? xrow + r : a.n_x_rows;
+                    a.yr[s + r] = p * a.M + r;
+                    a.xr[s + r] = valid ? xrow + r : a.n_x_rows;
                 }
             }
-            __syncthreads();  // cursors advanced, counts cleared for the next batch
+            slot += uint32_t(__popcll(m));
         }
     }
 }
@@ -178,6 +134,6 @@ extern "C" int iqk_route(const uint32_t *ids, int64_t n_pairs, int64_t num_exper
     a.M = uint32_t(rows_per_pair);
     a.ppx = uint32_t(pairs_per_x_row);
     a.n_x_rows = uint32_t(n_x_rows);
-    hipLaunchKernelGGL(route_kernel, dim3{1}, dim3{kRouteThreads}, 0, as_stream(stream), a);
+    hipLaunchKernelGGL(route_kernel, dim3{uint32_t(num_experts)}, dim3{kRouteThreads}, 0, as_stream(stream), a);
     return record_launch(hipGetLastError());
 }
