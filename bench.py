@@ -831,21 +831,21 @@ def main() -> int:
                 # each calibrated on a plain copy of known size
                 "traffic": traffic, "traffic_source": traffic_file.name if traffic else None,
                 "trace": "profiles/gemv_mfma_iq2_ks_routed_decode.md"}
-    # every priced cell: its ratios and the reference's gates
+    # every priced cell: its ratios and the reference's gates (kept short, so the whole line
+    # survives a tail of the output; `--json-out` has every figure)
     summary, gates = {}, {}
     for m, r in results.items():
         for c, cell in (r.get("cells") or {}).items():
             key = f"{m}_{c}" + (f"_x{r['tokens']}" if r.get("tokens", 1) != 1 else "")
-            summary[key] = {k: cell[k] for k in ("x_floor", "x_stream", "x_floor_grid", "within_bar_vs_grid_floor")
-                            if k in cell}
-            summary[key].update(us=cell["decode"]["median_us"], floor_us=cell["floor"]["median_us"],
-                                gb_per_s=cell["decode"]["gb_per_s"])
-            gates[key] = cell["gates"]
+            summary[key] = {k: round(cell[k], 3) for k in ("x_floor", "x_stream", "x_floor_grid") if k in cell}
+            summary[key]["us"] = round(cell["decode"]["median_us"], 2)
+            gates[key] = dict(cell["gates"])
+            if "within_bar_vs_grid_floor" in cell:
+                gates[key]["within_bar_vs_grid_floor"] = cell["within_bar_vs_grid_floor"]
     for m, r in (results.get("dequant") or {}).items():
         for c, cell in r.items():
             key = f"producer_{m}_{c}"
-            summary[key] = {"x_floor": cell["x_floor"], "us": cell["decode"]["median_us"],
-                            "floor_us": cell["floor"]["median_us"], "gb_per_s": cell["decode"]["gb_per_s"]}
+            summary[key] = {"x_floor": round(cell["x_floor"], 3), "us": round(cell["decode"]["median_us"], 2)}
             gates[key] = cell["gates"]
     if "verify" in results:
         summary["verify"] = {k: {m: v[m]["median_us"] for m in ("pairs", "sorted", "union")}
@@ -872,7 +872,10 @@ def main() -> int:
         "bars": {"decode_vs_own_floor": DECODE_BAR, "producer_vs_own_floor": PRODUCER_BAR,
                  "floor_band_gb_s": list(FLOOR_BAND_GBS)},
         "cells": summary,
-        "gates": gates,
+        # the gates each cell fails (floor_in_band, no_deleted_load_signature, within_bar,
+        # within_bar_vs_grid_floor); a cell that passes all of them is not listed
+        "gates_checked": len(gates),
+        "gates_failed": {k: [n for n, ok in g.items() if not ok] for k, g in gates.items() if not all(g.values())},
         "all_gates_pass": all(all(g.values()) for g in gates.values()),
         "elapsed_s": round(time.time() - t_start, 1),
     }
