@@ -12,12 +12,13 @@
 //
 // Work list: as the grouped GEMM, with group g = expert g: the slots (pair
 // rows) are sorted by expert, expert g owns [offs[g], offs[g+1]), and a block
-// takes one M-tile t of the list (64 slots) and one column block c (weight
-// rows [256c, 256c + 256) of the requested row range).  Blocks are dealt to
-// the eight XCDs in turn, so block b runs on XCD b % 8; the mapping gives
-// XCD b % 8 the column blocks of M-tile 8 (b / (8 C)) + b % 8 one after
-// another (C column blocks), and the activations they share stay in that
-// XCD's L2.
+// takes one M-tile of the list (64 slots) and one column block c (weight rows
+// [256c, 256c + 256) of the requested row range).  XCD x (blocks b with
+// b % 8 == x) takes a contiguous eighth of the M-tiles, each with all its
+// column blocks one after another, so the column blocks of a tile share its
+// activations in that XCD's L2 and an expert's M-tiles share its streams
+// there (dealing M-tile 8i + x to XCD x instead fetched 1.32x the unique
+// bytes from HBM, an expert's tiles landing on several XCDs).
 //
 // Tile: 512 threads, eight wavefronts.  Wavefront w owns weight rows
 // 32w .. 32w+31 of the block (the 32 columns of v_mfma_f32_32x32x16_f16) for
@@ -63,9 +64,10 @@ constexpr int kFusedBM = 64;                     // slots per block
 constexpr int kFusedBN = 32 * kFusedWaves;       // weight rows per block
 constexpr int kFusedKS = 128;                    // reduction elements per step
 constexpr int kXStride = 2 * kFusedKS + 16;      // LDS bytes per staged activation row
-constexpr int kXBytes = kFusedBM * 2 * kFusedKS / kFusedThreads;  // activation bytes a thread stages per step
-constexpr int kXSegs = 2 * kFusedKS / kXBytes;                    // threads per staged row
-static_assert(kXBytes % 16 == 0 && kFusedThreads >= 256, "whole 16-byte chunks; the work-list scan needs 256 threads");
+constexpr int kXChunks = 2 * kFusedKS / 16;      // 16-byte chunks of a staged row per step
+constexpr int kXRows = kFusedThreads / kXChunks; // rows one staging pass covers
+constexpr int kXPer = kFusedBM / kXRows;         // staging passes a step
+static_assert(kFusedBM % kXRows == 0 && kFusedThreads >= 256, "whole staging passes; the work-list scan needs 256 threads");
 
 struct FusedArgs {
     const uint16_t *x;
@@ -102,18 +104,30 @@ struct FusedScales {
     uint8_t dv[DV_IN_LDS ? kFusedBN * DV_S : 4];
 };
 
-// Copy `rows` rows of a plane (BYTES a row, consecutive in global memory)
-// into LDS rows of STRIDE bytes, in 32-bit units where the rows are whole
-// dwords (every plane but IQ2_KS's per-row scale), else 16-bit units.
+// Copy `rows` (1 .. kFusedBN) rows of a plane (BYTES a row, consecutive in
+// global memory) into LDS rows of STRIDE bytes, in 32-bit units where the
+// rows are whole dwords (every plane but IQ2_KS's per-row scale), else
+// 16-bit units.  Straight-line: every thread issues all its loads, then all
+// its stores, so the plane costs one memory latency; units past `rows`
+// re-read the last unit and land in LDS rows nobody stores from.
 template <int BYTES, int STRIDE>
 __device__ __forceinline__ void copy_plane(const uint8_t *src, int rows, uint8_t *dst, int tid) {
     using Unit = std::conditional_t<BYTES % 4 == 0, uint32_t, uint16_t>;
     static_assert(BYTES % sizeof(Unit) == 0 && STRIDE % sizeof(Unit) == 0, "whole units a row");
     constexpr int UNITS_PER_ROW = BYTES / sizeof(Unit);
-    const int units = rows * UNITS_PER_ROW;
-    for (int u = tid; u < units; u += kFusedThreads) {
-        const int r = u / UNITS_PER_ROW, c = u - r * UNITS_PER_ROW;
-        *reinterpret_cast<Unit *>(dst + r * STRIDE + sizeof(Unit) * c) = reinterpret_cast<const Unit *>(src)[u];
+    constexpr int UNITS = kFusedBN * UNITS_PER_ROW;
+    constexpr int PER = (UNITS + kFusedThreads - 1) / kFusedThreads;
+    const int last = rows * UNITS_PER_ROW - 1;
+    Unit v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) v[i] = reinterpret_cast<const Unit *>(src)[min(tid + kFusedThreads * i, last)];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int u = tid + kFusedThreads * i;
+        if (UNITS % kFusedThreads == 0 || u < UNITS) {
+            const int r = u / UNITS_PER_ROW, c = u - r * UNITS_PER_ROW;
+            *reinterpret_cast<Unit *>(dst + r * STRIDE + sizeof(Unit) * c) = v[i];
+        }
     }
 }
 
@@ -196,10 +210,15 @@ void fused_gemm_kernel(FusedArgs a) {
 
     const int tid = threadIdx.x;
     const uint32_t ncb = (a.N + kFusedBN - 1) / kFusedBN;  // column blocks
-    const uint32_t bq = blockIdx.x >> 3, xcd = blockIdx.x & 7u;
-    const uint32_t tile = 8 * (bq / ncb) + xcd, cblock = bq % ncb;
+    const uint32_t tiles = count_mtiles<kFusedBM, kFusedThreads>(a.offs, a.n_groups, ts);
+    const uint32_t per_xcd = (tiles + 7) / 8;
+    const uint32_t xcd = blockIdx.x & 7u, j = blockIdx.x >> 3;
+    if (j / ncb >= per_xcd) return;  // surplus block (uniform)
+    const uint32_t tile = xcd * per_xcd + j / ncb, cblock = j % ncb;
+    if (tile >= tiles) return;
     uint32_t g, mtile;
-    if (!find_mtile<kFusedBM, kFusedThreads>(a.offs, a.n_groups, tile, ts, g, mtile)) return;  // surplus block
+    if (!find_mtile<kFusedBM, kFusedThreads>(a.offs, a.n_groups, tile, ts, g, mtile)) return;
+    g = __builtin_amdgcn_readfirstlane(g);  // uniform (read from LDS): the stream bases stay scalar
 
     // Offsets and row indices are device data: a slot outside [0, n_slots)
     // is never stored, a row outside x is never read (its output row is NaN),
@@ -231,67 +250,85 @@ void fused_gemm_kernel(FusedArgs a) {
             copy_plane<S::DV, S::DV_S>(static_cast<const uint8_t *>(a.s3) + row0 * S::DV, rows_here, sc.dv, tid);
     }
 
-    // activation staging: thread t moves kXBytes of slot row t / kXSegs per step
-    const int xrow_l = tid / kXSegs, xseg = tid % kXSegs;
-    const uint32_t xp = m0 + uint32_t(xrow_l);
-    const uint32_t xrow = xp < gend ? a.xr[xp] : a.n_x_rows;
-    const bool xv = xrow < a.n_x_rows;
-    const uint8_t *xsrc = reinterpret_cast<const uint8_t *>(a.x) + size_t(xv ? xrow : 0u) * K * 2 + kXBytes * xseg;
+    // activation staging: thread t moves 16-byte chunk t % kXChunks of slot
+    // rows t / kXChunks + kXRows i a step, so the eight lanes of each LDS
+    // store phase write 128 contiguous bytes (a thread's two chunks side by
+    // side had every store phase hit each bank twice).  Byte offsets into x
+    // are 32-bit (the entry point refuses an x of 4 GiB or more).
     // A row past the tile's last slot feeds only MFMA rows that are never
     // stored, so IQ1_S_R4 neither loads nor stages it (its LDS row keeps
     // whatever it held): a partial tile (most tiles of a skewed routing)
-    // stages only its slots, and the boundary is uniform per wavefront but
-    // for one.  Measured on the 2048-token Zipf prefill: IQ1_S_R4 -4%; the
-    // IQ2 members, whose step the branch splits for the scheduler, +1 to +2%,
-    // so they stage every row.
-    const bool xlive = !IQ1 || xp < gend;
-    if (xseg == 0) {  // one thread a slot: the epilogue's destination, read once
-        uint32_t dst = kNoStore;
-        if (xp < gend) {
-            const uint32_t yrow = a.yr ? a.yr[xp] : xp;
-            if (yrow < a.n_slots) dst = yrow | (xv ? 0x80000000u : 0u);
+    // stages only its slots.  Measured on the 2048-token Zipf prefill:
+    // IQ1_S_R4 -4%; the IQ2 members, whose step the branch splits for the
+    // scheduler, +1 to +2%, so they stage every row.
+    const int xrow_l = tid / kXChunks, xchunk = tid % kXChunks;
+    const uint8_t *xbase = reinterpret_cast<const uint8_t *>(a.x);
+    uint32_t xoff[kXPer];
+    bool xlive[kXPer];
+#pragma unroll
+    for (int i = 0; i < kXPer; ++i) {
+        const int row = xrow_l + kXRows * i;
+        const uint32_t xp = m0 + uint32_t(row);
+        const uint32_t xrow = xp < gend ? a.xr[xp] : a.n_x_rows;
+        const bool xv = xrow < a.n_x_rows;
+        // a dead slot reads row 0 (the entry point refuses an empty x); its
+        // products feed only its own output row, never stored as a value
+        xoff[i] = (xv ? xrow : 0u) * uint32_t(2 * K) + uint32_t(16 * xchunk);
+        xlive[i] = !IQ1 || xp < gend;
+        if (xchunk == 0) {  // one thread a slot: the epilogue's destination, read once
+            uint32_t dst = kNoStore;
+            if (xp < gend) {
+                const uint32_t yrow = a.yr ? a.yr[xp] : xp;
+                if (yrow < a.n_slots) dst = yrow | (xv ? 0x80000000u : 0u);
+            }
+            slot_dst[row] = dst;
         }
-        slot_dst[xrow_l] = dst;
     }
     const auto load_x = [&](int s, uint4_t *v) {
-        if (!xlive) return;
 #pragma unroll
-        for (int i = 0; i < kXBytes / 16; ++i) v[i] = load_u4(xsrc + 2 * kFusedKS * s + 16 * i);
+        for (int i = 0; i < kXPer; ++i)
+            if (xlive[i]) v[i] = load_u4(xbase + xoff[i] + uint32_t(2 * kFusedKS * s));
     };
     // Each 8-element chunk is stored in the order (0,4,1,5,2,6,3,7), the
     // order expand_word_paired gives the weights.
     const auto store_x = [&](int buf, const uint4_t *v) {
-        if (!xlive) return;
-        uint8_t *dst = xs[buf] + xrow_l * kXStride + kXBytes * xseg;
+        uint8_t *dst = xs[buf] + xrow_l * kXStride + 16 * xchunk;
 #pragma unroll
-        for (int i = 0; i < kXBytes / 16; ++i)
-            *reinterpret_cast<uint4_t *>(dst + 16 * i) =
-                uint4_t{perm(v[i].z, v[i].x, 0x05040100u), perm(v[i].z, v[i].x, 0x07060302u),
-                        perm(v[i].w, v[i].y, 0x05040100u), perm(v[i].w, v[i].y, 0x07060302u)};
+        for (int i = 0; i < kXPer; ++i)
+            if (xlive[i])
+                *reinterpret_cast<uint4_t *>(dst + kXRows * kXStride * i) =
+                    uint4_t{perm(v[i].z, v[i].x, 0x05040100u), perm(v[i].z, v[i].x, 0x07060302u),
+                            perm(v[i].w, v[i].y, 0x05040100u), perm(v[i].w, v[i].y, 0x07060302u)};
     };
 
-    // this lane's weight row and code words
+    // this lane's weight row and code words; a row past out_features reads
+    // the block's first row.  The block's first row of each plane is a
+    // uniform base, the lane's offsets from it are 32-bit (the entry point
+    // refuses an expert plane of 4 GiB or more).  IQ2 members: the step's
+    // four code words; IQ1_S_R4: the two blocks' index words and their qh
+    // words (blocks 4s + 2kg, +1).
     const int wave = tid >> 6, l = tid & 63, ln = l & 31, kg = l >> 5;
     const int lrow = 32 * wave + ln;
     const bool wv = lrow < rows_here;
-    const size_t wrow = row0 + (wv ? lrow : 0);  // in-bounds row for the loads
-    // IQ2 members: the step's four code words; IQ1_S_R4: the two blocks'
-    // index words and their qh words (blocks 4s + 2kg, +1)
-    const uint8_t *qsrc = static_cast<const uint8_t *>(a.s0) + (IQ1 ? wrow * (K / 8) + 8 * kg : wrow * (K / 4) + 16 * kg);
-    const uint8_t *hsrc = static_cast<const uint8_t *>(a.s1) + (wrow * (K / 16) + 4 * kg);
+    constexpr uint32_t QROW = IQ1 ? K / 8 : K / 4;  // code-plane bytes a row
+    const uint8_t *qbase = static_cast<const uint8_t *>(a.s0) + row0 * QROW;
+    const uint8_t *hbase = static_cast<const uint8_t *>(a.s1) + row0 * (K / 16);
+    const uint32_t wl = wv ? uint32_t(lrow) : 0u;
+    const uint32_t qoff = wl * QROW + uint32_t((IQ1 ? 8 : 16) * kg), hoff = wl * uint32_t(K / 16) + uint32_t(4 * kg);
     const auto load_q = [&](int s) {
         if constexpr (IQ1) {
-            const uint2_t iw = *reinterpret_cast<const uint2_t *>(qsrc + 16 * s);
-            return uint4_t{iw.x, iw.y, *reinterpret_cast<const uint32_t *>(hsrc + 8 * s), 0u};
+            const uint2_t iw = *reinterpret_cast<const uint2_t *>(qbase + qoff + uint32_t(16 * s));
+            return uint4_t{iw.x, iw.y, *reinterpret_cast<const uint32_t *>(hbase + hoff + uint32_t(8 * s)), 0u};
         } else {
-            return load_u4(qsrc + 32 * s);
+            return load_u4(qbase + qoff + uint32_t(32 * s));
         }
     };
 
-    uint4_t xa[kXBytes / 16];
+    uint4_t xa[kXPer];
     load_x(0, xa);
     // IQ2_K without a dv plane in LDS: this lane's dv words, one per four steps
-    const uint32_t *dvp = reinterpret_cast<const uint32_t *>(static_cast<const uint8_t *>(a.s3) + wrow * (K / 128));
+    const uint32_t *dvp = reinterpret_cast<const uint32_t *>(static_cast<const uint8_t *>(a.s3) + row0 * (K / 128) +
+                                                             wl * uint32_t(K / 128));
     constexpr bool DV_WORDS = MEMBER == IQ2_K && !S::DV_IN_LDS;
     uint32_t dvw = DV_WORDS ? dvp[0] : 0u, dvn = 0u;
     uint4_t q = load_q(0), qn;
@@ -304,18 +341,19 @@ void fused_gemm_kernel(FusedArgs a) {
     if constexpr (MEMBER == IQ2_KS)
         d = half_of_bits(*reinterpret_cast<const uint16_t *>(sc.dv + lrow * S::DV_S));
     else if constexpr (IQ1)
-        d = half_of_bits(static_cast<const uint16_t *>(a.s2)[wrow]);
-
-    float16_t acc[2];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[mb][r] = 0.f;
+        d = half_of_bits(static_cast<const uint16_t *>(a.s2)[row0 + wl]);
 
     // A tile of at most 32 real slots (most experts of a skewed routing)
-    // runs the second slot block's MFMAs for nothing: skip them.
+    // runs the second slot block's MFMAs for nothing: skip them (its slots
+    // 32 .. 63 are past the tile's end, never stored, so their accumulators
+    // do not exist).
     const auto run_steps = [&](auto slot_blocks) {
         constexpr int MB = decltype(slot_blocks)::value;
+        float16_t acc[MB];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[mb][r] = 0.f;
         for (int s = 0; s < STEPS; ++s) {
             const bool more = s + 1 < STEPS;
             if (more) {
@@ -372,25 +410,25 @@ void fused_gemm_kernel(FusedArgs a) {
             }
             __syncthreads();
         }
+
+        // D layout (32x32): lane l, register r holds row 8(r/4) + 4(l/32) +
+        // r%4 of column l % 32.
+        if (!wv) return;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t dst = slot_dst[32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3)];
+                if (dst != kNoStore)
+                    a.y[size_t(dst & 0x7fffffffu) * a.N + n0 + lrow] =
+                        (dst >> 31) ? uint16_t(float_to_half_bits(acc[mb][r])) : kHalfNaN;
+            }
+        }
     };
     if (gend - m0 <= 32)  // uniform per block
         run_steps(std::integral_constant<int, 1>{});
     else
         run_steps(std::integral_constant<int, 2>{});
-
-    // D layout (32x32): lane l, register r holds row 8(r/4) + 4(l/32) + r%4
-    // of column l % 32.
-    if (!wv) return;
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t dst = slot_dst[32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3)];
-            if (dst != kNoStore)
-                a.y[size_t(dst & 0x7fffffffu) * a.N + n0 + lrow] =
-                    (dst >> 31) ? uint16_t(float_to_half_bits(acc[mb][r])) : kHalfNaN;
-        }
-    }
 }
 
 template <int MEMBER>
@@ -417,12 +455,15 @@ extern "C" int iqk_fused_gemm(int member, int64_t in_features, int64_t out_featu
     if (!member_ok(member)) return IQK_ERR_MEMBER;
     if (!width_sized(in_features)) return IQK_ERR_GEOMETRY;
     if (out_features <= 0 || out_features > (int64_t(1) << 24)) return IQK_ERR_GEOMETRY;
+    // 32-bit offsets within an expert's code plane (in/4 bytes a row) and x
+    if (out_features * (in_features / 4) >= (int64_t(1) << 32)) return IQK_ERR_GEOMETRY;
     if (row_start < 0 || rows <= 0 || row_start + rows > out_features) return IQK_ERR_GEOMETRY;
     if (num_experts <= 0 || num_experts > (int64_t(1) << 20)) return IQK_ERR_ARGUMENT;
     if (n_slots < 0 || n_slots > (int64_t(1) << 30) || n_x_rows < 0 || n_x_rows > 0xffffffffll)
         return IQK_ERR_ARGUMENT;
     if (n_slots == 0) return IQK_OK;
     if (!x || !y || !group_offsets || !x_rows || !streams_ok(streams, n_streams, member)) return IQK_ERR_ARGUMENT;
+    if (n_x_rows == 0 || n_x_rows * in_features * 2 >= (int64_t(1) << 32)) return IQK_ERR_ARGUMENT;
     FusedArgs a;
     a.x = static_cast<const uint16_t *>(x);
     a.s0 = streams[0]; a.s1 = streams[1]; a.s2 = streams[2];
