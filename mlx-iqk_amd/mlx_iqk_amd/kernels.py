@@ -391,6 +391,13 @@ FUSED_MEMBERS = MEMBERS
 """Members the fused prefill contraction covers (all three)."""
 
 
+def fused_fits(n_x_rows: int, in_features: int, out_features: int) -> bool:
+    """Whether the fused prefill serves these operands: its lane offsets are
+    32-bit, within one expert's code plane (``in/4`` bytes a row) and within
+    x, so both stay below 4 GiB (the entry point refuses larger ones)."""
+    return out_features * (in_features // 4) < 1 << 32 and 0 < n_x_rows and n_x_rows * in_features * 2 < 1 << 32
+
+
 def fused_matmul(member: str, x: torch.Tensor, streams: list[torch.Tensor], num_experts: int, out_features: int,
                  group_offsets: torch.Tensor, x_rows: torch.Tensor, y_rows: torch.Tensor | None = None, *,
                  row_start: int = 0, rows: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -435,6 +442,6 @@ __all__ = [
     "DEQUANT_THREADS", "IQ2_MEMBERS", "MEMBERS", "ROWS_PER_TG",
     "SUPPORTED_IN_FEATURES", "TABLE_INPUT_NAMES", "WEIGHTS_PER_LANE", "IqkKernelError",
     "check_dequant_geometry", "check_gemv_geometry", "check_streams", "dequant", "dequant_input_names",
-    "FUSED_MEMBERS", "ROUTE_MAX_EXPERTS", "check_iq2_member", "fused_matmul", "gemv", "pack", "route", "stream_floor", "gemv_input_names", "gemv_sorted", "grouped_gemm",
+    "FUSED_MEMBERS", "ROUTE_MAX_EXPERTS", "check_iq2_member", "fused_fits", "fused_matmul", "gemv", "pack", "route", "stream_floor", "gemv_input_names", "gemv_sorted", "grouped_gemm",
     "stream_dtypes",
 ]

@@ -278,7 +278,8 @@ class IqkSwitchLinear(torch.nn.Module):
         xflat = xb.reshape(-1, self.in_features).contiguous()
         E = self.num_experts
         offsets, x_rows, y_rows = self._route(tuple(xb.shape[:-2]), batch, indices, M, xflat.shape[0])
-        if self.fused_prefill and self.member in kernels.FUSED_MEMBERS:
+        if self.fused_prefill and self.member in kernels.FUSED_MEMBERS and kernels.fused_fits(
+                xflat.shape[0], self.in_features, self.out_features):
             y = kernels.fused_matmul(self.member, xflat, self._streams(), E, self.out_features, offsets, x_rows,
                                      y_rows, row_start=start, rows=rows)
             return y.reshape(tuple(batch) + (M, rows))

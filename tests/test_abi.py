@@ -140,6 +140,10 @@ def test_fused_gemm_refuses_bad_arguments(lib):
     assert f(1, 4096, 2048, 8, None, 4, streams, 4, 0, 2048, p, p, None, 4, p, None) == _native.ERR_ARGUMENT
     assert f(1, 4096, 2048, 8, p, 4, streams, 4, 0, 2048, None, p, None, 4, p, None) == _native.ERR_ARGUMENT
     assert f(1, 4096, 2048, 8, p, 4, streams, 4, 0, 2048, p, p, None, 0, p, None) == _native.OK
+    # 32-bit offsets: an expert plane or an x of 4 GiB or more, and an empty x, are refused
+    assert f(0, 4096, 1 << 22, 8, p, 4, streams, 5, 0, 2048, p, p, None, 4, p, None) == _native.ERR_GEOMETRY
+    assert f(0, 4096, 2048, 8, p, 1 << 19, streams, 5, 0, 2048, p, p, None, 4, p, None) == _native.ERR_ARGUMENT
+    assert f(0, 4096, 2048, 8, p, 0, streams, 5, 0, 2048, p, p, None, 4, p, None) == _native.ERR_ARGUMENT
 
 
 def test_route_refuses_bad_arguments(lib):
