@@ -35,8 +35,12 @@ def _reference(ids: np.ndarray, E: int, M: int, ppx: int, n_x_rows: int):
     return offs, x_rows, y_rows
 
 
+# past 16384 pairs a wavefront's share exceeds the ids it holds (2048), and
+# its second pass reloads them round by round: 40000 (three rounds) and
+# 16385 at the most experts the route serves
 @pytest.mark.parametrize("P,E,M,ppx", [(12288, 256, 1, 1), (12288, 256, 1, 6), (300, 8, 3, 1), (1, 1, 1, 1),
-                                       (5000, 4096, 2, 5), (1023, 33, 1, 1), (2049, 256, 1, 2)])
+                                       (5000, 4096, 2, 5), (1023, 33, 1, 1), (2049, 256, 1, 2),
+                                       (40000, 256, 1, 8), (16385, 4096, 1, 1)])
 def test_route_matches_a_stable_sort(device, P, E, M, ppx):
     print(f"route P={P} E={E} M={M} ppx={ppx}", flush=True)
     rng = np.random.default_rng(P + E)
