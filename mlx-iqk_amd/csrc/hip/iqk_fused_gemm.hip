@@ -156,6 +156,28 @@ constexpr Iq2kProducts make_iq2k_products() {
 
 __constant__ const Iq2kProducts kIq2kProducts = make_iq2k_products();
 
+// IQ1_S_R4's exact pool products n_c = (2s + 1) (g_c + shift), g = -1 .. 2,
+// shift = 1/8 (negative when qh bit 15 is set), by qh bits 12-15 (s | sign
+// << 3): at most 8 significant bits, so exact in fp16, and d x n rounded
+// once is the producer's f32 chain d (2s+1) (g + shift) rounded once.
+struct Iq1Products {
+    uint32_t w[2 * 16];
+};
+
+constexpr Iq1Products make_iq1_products() {
+    Iq1Products t{};
+    for (int e = 0; e < 16; ++e) {
+        const int s = e & 7, sign = e & 8 ? -1 : 1;
+        for (int c = 0; c < 4; ++c) {
+            const _Float16 n = _Float16(float((2 * s + 1) * (8 * (c - 1) + sign)) / 8.f);
+            t.w[2 * e + c / 2] |= uint32_t(__builtin_bit_cast(uint16_t, n)) << (16 * (c % 2));
+        }
+    }
+    return t;
+}
+
+__constant__ const Iq1Products kIq1Products = make_iq1_products();
+
 // The pool d x n_c from the products at byte `off` of the LDS table.  The
 // words pass as scalars: __builtin_bit_cast of a vector element (n.y of a
 // uint2_t) reads the vector's first element in this compiler.
@@ -217,16 +239,17 @@ __device__ __forceinline__ void fused_pools(const FusedScales<MEMBER, K> &sc, in
 }
 
 // IQ1_S_R4 at one step: blocks b = 0, 1 of the lane (index bytes q[b], qh
-// word b of q.z).  Pools p[2b], p[2b+1] are block b's (dl = d (2s+1), values
-// g + shift, as the producer), and word 2b+t holds the grid codes of the
-// block's 8-weight groups 2t and 2t+1.
-__device__ __forceinline__ void fused_iq1(uint4_t q, const uint16_t *grid, _Float16 d, Pool *p, uint32_t *words) {
+// word b of q.z).  Pools p[2b], p[2b+1] are block b's (d times the products
+// (2s+1) (g + shift) from the LDS table `ptab`: the producer's values), and
+// word 2b+t holds the grid codes of the block's 8-weight groups 2t and 2t+1.
+__device__ __forceinline__ void fused_iq1(uint4_t q, const uint16_t *grid, const uint2_t *ptab, _Float16 d, Pool *p,
+                                          uint32_t *words) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
         const uint32_t qw = q[b], h = (q.z >> (16 * b)) & 0xffffu;
-        const float dl = float(d) * float(int(2 * ((h >> 12) & 7u) + 1));
-        const float sh = (h & 0x8000u) ? -0.125f : 0.125f;
-        p[2 * b] = make_pool(dl, -1.f + sh, 0.f + sh, 1.f + sh, 2.f + sh);  // grid field 3 never occurs
+        // grid field 3 never occurs: four products, by qh bits 12-15
+        const uint2_t n = ptab[(h >> 12) & 15u];
+        p[2 * b] = scale_products(uint32_t(n.x), uint32_t(n.y), d);
         p[2 * b + 1] = p[2 * b];
         uint32_t c[4];
 #pragma unroll
@@ -251,7 +274,7 @@ void fused_gemm_kernel(FusedArgs a) {
     // per slot of the tile: its output row, bit 31 set when its activations
     // are real (else its output row is NaN), or kNoStore
     __shared__ uint32_t slot_dst[kFusedBM];
-    __shared__ uint2_t ptab[MEMBER == IQ2_K ? 32 : 1];  // IQ2_K's pool products
+    __shared__ uint2_t ptab[MEMBER == IQ2_K ? 32 : IQ1 ? 16 : 1];  // IQ2_K's and IQ1_S_R4's pool products
     constexpr uint32_t kNoStore = 0x7fffffffu;  // above any row (n_slots <= 2^30)
     __shared__ __attribute__((aligned(16))) std::conditional_t<IQ1, FusedGrid, S> sc;
 
@@ -281,6 +304,8 @@ void fused_gemm_kernel(FusedArgs a) {
 
     if constexpr (MEMBER == IQ2_K) {
         if (tid < 32) ptab[tid] = reinterpret_cast<const uint2_t *>(kIq2kProducts.w)[tid];
+    } else if constexpr (IQ1) {
+        if (tid < 16) ptab[tid] = reinterpret_cast<const uint2_t *>(kIq1Products.w)[tid];
     }
     // scale planes of the block's rows (IQ1_S_R4: the grid codes)
     if constexpr (IQ1) {
@@ -416,7 +441,7 @@ void fused_gemm_kernel(FusedArgs a) {
             Pool p[4];
             uint32_t words[4];
             if constexpr (IQ1) {
-                fused_iq1(q, sc.codes, d, p, words);
+                fused_iq1(q, sc.codes, ptab, d, p, words);
             } else {
                 fused_pools<MEMBER, K>(sc, lrow, s, kg, d, dvw, ptab, p);
 #pragma unroll
