@@ -27,6 +27,7 @@ namespace iqk {
 
 constexpr int kPackThreads = 256;
 constexpr int kPackLdsBytes = 40960;
+constexpr int kPackBatch = 8;  // wire dwords a thread loads before it stores them
 
 struct PackArgs {
     const uint8_t *wire;
@@ -70,14 +71,31 @@ __device__ __forceinline__ void relayout_codes(const uint32_t *q, uint32_t *out)
 
 template <int MEMBER>
 __global__ __launch_bounds__(kPackThreads) void pack_kernel(PackArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kPackLdsBytes + 16];
+    // the block's wire rows (+ 16 bytes, read past by lds_words): sized at
+    // launch, so a CU holds as many blocks as their rows allow
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x;
     const uint32_t r0 = blockIdx.x * a.rows_per_block;
     const uint32_t rows_here = min(a.rows_per_block, a.rows - r0);
     const uint64_t first = uint64_t(r0) * a.row_bytes;  // 4-byte aligned (even rows per block, even row bytes)
     const uint32_t bytes = rows_here * a.row_bytes;
     const uint32_t *src = reinterpret_cast<const uint32_t *>(a.wire + first);
-    for (uint32_t i = tid; i < bytes / 4; i += kPackThreads) reinterpret_cast<uint32_t *>(lds)[i] = src[i];
+    // in batches of kPackBatch loads a thread, all issued before any store,
+    // so the copy costs a memory latency a batch, not one per dword
+    const uint32_t words = bytes / 4;
+    for (uint32_t i0 = 0; i0 < words; i0 += kPackBatch * kPackThreads) {
+        uint32_t v[kPackBatch];
+#pragma unroll
+        for (int j = 0; j < kPackBatch; ++j) {
+            const uint32_t i = i0 + uint32_t(j * kPackThreads + tid);
+            v[j] = src[min(i, words - 1u)];  // past the end: re-reads the last dword, never stored
+        }
+#pragma unroll
+        for (int j = 0; j < kPackBatch; ++j) {
+            const uint32_t i = i0 + uint32_t(j * kPackThreads + tid);
+            if (i < words) reinterpret_cast<uint32_t *>(lds)[i] = v[j];
+        }
+    }
     if ((bytes & 3u) && tid == 0)  // an odd last row leaves one 16-bit unit
         *reinterpret_cast<uint16_t *>(lds + (bytes & ~3u)) = *reinterpret_cast<const uint16_t *>(a.wire + first + (bytes & ~3u));
     __syncthreads();
@@ -181,11 +199,12 @@ extern "C" int iqk_pack(int member, int64_t in_features, int64_t rows, const voi
     a.nb = uint32_t(nb);
     a.rows_per_block = uint32_t(units * unit);
     const dim3 grid{uint32_t((rows + a.rows_per_block - 1) / a.rows_per_block)}, blk{kPackThreads};
+    const size_t lds = (size_t(a.rows_per_block) * a.row_bytes + 16 + 15) / 16 * 16;
     hipStream_t st = as_stream(stream);
     switch (member) {
-        case IQK_MEMBER_IQ2_KS: hipLaunchKernelGGL(pack_kernel<IQ2_KS>, grid, blk, 0, st, a); break;
-        case IQK_MEMBER_IQ2_K: hipLaunchKernelGGL(pack_kernel<IQ2_K>, grid, blk, 0, st, a); break;
-        default: hipLaunchKernelGGL(pack_kernel<IQ1_S_R4>, grid, blk, 0, st, a); break;
+        case IQK_MEMBER_IQ2_KS: hipLaunchKernelGGL(pack_kernel<IQ2_KS>, grid, blk, lds, st, a); break;
+        case IQK_MEMBER_IQ2_K: hipLaunchKernelGGL(pack_kernel<IQ2_K>, grid, blk, lds, st, a); break;
+        default: hipLaunchKernelGGL(pack_kernel<IQ1_S_R4>, grid, blk, lds, st, a); break;
     }
     return record_launch(hipGetLastError());
 }
