@@ -107,6 +107,35 @@ def check_streams(member: str, streams: list[torch.Tensor], num_experts: int, ou
     return device
 
 
+class CheckedStreams:
+    """A member's streams for one geometry, checked once (count, shapes, dtypes,
+    one GPU, contiguity): the device and the pointer array the launchers pass.
+    Every launcher takes one in place of the stream list and skips its checks;
+    it stays valid while the tensors do (``IqkSwitchLinear`` drops its copy
+    whenever a stream is reassigned or the module is moved)."""
+
+    __slots__ = ("key", "device", "ptrs", "count")
+
+    def __init__(self, member: str, streams: list[torch.Tensor], num_experts: int, out_features: int,
+                 in_features: int):
+        self.device = check_streams(member, streams, num_experts, out_features, in_features)
+        self.key = (member, int(num_experts), int(out_features), int(in_features))
+        self.ptrs = _native.pointer_array([t.data_ptr() for t in streams])
+        self.count = len(streams)
+
+
+def _streams_for(member: str, streams, num_experts: int, out_features: int, in_features: int):
+    """The device, pointer array and count of a launch's streams: a
+    CheckedStreams of this geometry as is, a list checked now."""
+    if isinstance(streams, CheckedStreams):
+        if streams.key != (member, int(num_experts), int(out_features), int(in_features)):
+            raise IqkKernelError(f"streams checked for {streams.key}, used for "
+                                 f"{(member, num_experts, out_features, in_features)}")
+        return streams.device, streams.ptrs, streams.count
+    device = check_streams(member, streams, num_experts, out_features, in_features)
+    return device, _native.pointer_array([t.data_ptr() for t in streams]), len(streams)
+
+
 def gemv(member: str, x: torch.Tensor, streams: list[torch.Tensor], sel: torch.Tensor, pairs_per_row: int,
          num_experts: int, out_features: int, *, floor: bool | str = False,
          out: torch.Tensor | None = None) -> torch.Tensor:
@@ -119,7 +148,7 @@ def gemv(member: str, x: torch.Tensor, streams: list[torch.Tensor], sel: torch.T
     check_member(member)
     n = int(x.shape[-1])
     check_gemv_geometry(n, out_features)
-    device = check_streams(member, streams, num_experts, out_features, n)
+    device, ptrs, n_streams = _streams_for(member, streams, num_experts, out_features, n)
     _require_cuda(x, "x", torch.float16, device)
     _require_cuda(sel, "sel", (torch.int32, torch.uint32), device)
     if x.dim() != 2 or sel.dim() != 1:
@@ -138,7 +167,6 @@ def gemv(member: str, x: torch.Tensor, streams: list[torch.Tensor], sel: torch.T
         return out
     lib = _native.load()
     fn = lib.iqk_gemv_floor_grid if floor == "grid" else lib.iqk_gemv_floor if floor else lib.iqk_gemv
-    ptrs = _native.pointer_array([t.data_ptr() for t in streams])
     # gridDim.y carries the pair index: launch in pair chunks that keep whole
     # activation rows together.
     limit = (65535 // pairs_per_row) * pairs_per_row
@@ -146,7 +174,7 @@ def gemv(member: str, x: torch.Tensor, streams: list[torch.Tensor], sel: torch.T
     for m0 in range(0, mats, limit):
         cnt = min(limit, mats - m0)
         rc = fn(_native.MEMBER_IDS[member], n, out_features, num_experts,
-                x.data_ptr() + (m0 // pairs_per_row) * n * 2, ptrs, len(streams),
+                x.data_ptr() + (m0 // pairs_per_row) * n * 2, ptrs, n_streams,
                 sel.data_ptr() + 4 * m0, pairs_per_row, cnt, out.data_ptr() + m0 * out_features * 2, stream)
         _native.check(rc, f"iqk_gemv{'_floor' if floor else ''}({member}, {n}x{out_features})")
     return out
@@ -196,7 +224,7 @@ def gemv_sorted(member: str, x: torch.Tensor, streams: list[torch.Tensor], sorte
     check_iq2_member(member)
     n = int(x.shape[-1])
     check_gemv_geometry(n, out_features)
-    device = check_streams(member, streams, num_experts, out_features, n)
+    device, ptrs, n_streams = _streams_for(member, streams, num_experts, out_features, n)
     _require_cuda(x, "x", torch.float16, device)
     _require_cuda(sorted_ids, "sorted_ids", (torch.int32, torch.uint32), device)
     _require_cuda(toks, "toks", (torch.int32, torch.uint32), device)
@@ -215,14 +243,13 @@ def gemv_sorted(member: str, x: torch.Tensor, streams: list[torch.Tensor], sorte
         return out
     lib = _native.load()
     fn = lib.iqk_gemv_union if union else lib.iqk_gemv_sorted
-    ptrs = _native.pointer_array([t.data_ptr() for t in streams])
     stream = _stream_ptr(device)
     # The pair index rides gridDim.z: chunks of at most 65535 pairs.  A run of
     # equal ids split by a chunk boundary is read once per chunk.
     for m0 in range(0, mats, 65535):
         cnt = min(65535, mats - m0)
         rc = fn(_native.MEMBER_IDS[member], n, out_features, num_experts, x.data_ptr(), int(x.shape[0]), ptrs,
-                len(streams), sorted_ids.data_ptr() + 4 * m0, toks.data_ptr() + 4 * m0, cnt,
+                n_streams, sorted_ids.data_ptr() + 4 * m0, toks.data_ptr() + 4 * m0, cnt,
                 out.data_ptr() + m0 * out_features * 2, stream)
         _native.check(rc, f"iqk_gemv_{'union' if union else 'sorted'}({member}, {n}x{out_features})")
     return out
@@ -247,7 +274,7 @@ def dequant(member: str, streams: list[torch.Tensor], num_experts: int, out_feat
         raise IqkKernelError(f"row range [{row_start}, {row_start + rows}) is outside out_features {out_features}")
     if floor and (row_start or rows != out_features):
         raise IqkKernelError("the producer's floor covers full experts only")
-    device = check_streams(member, streams, num_experts, out_features, in_features)
+    device, ptrs, n_streams = _streams_for(member, streams, num_experts, out_features, in_features)
     if slot_of_expert is None:
         n_slots = num_experts if n_slots is None else int(n_slots)
         if n_slots < num_experts:
@@ -268,15 +295,14 @@ def dequant(member: str, streams: list[torch.Tensor], num_experts: int, out_feat
         if tuple(out.shape) != shape:
             raise IqkKernelError(f"out must be {shape}, got {tuple(out.shape)}")
     lib = _native.load()
-    ptrs = _native.pointer_array([t.data_ptr() for t in streams])
     mid = _native.MEMBER_IDS[member]
     if ranged:
-        rc = lib.iqk_dequant_rows(mid, in_features, out_features, num_experts, ptrs, len(streams), row_start,
+        rc = lib.iqk_dequant_rows(mid, in_features, out_features, num_experts, ptrs, n_streams, row_start,
                                   rows, slot_ptr, int(n_slots), out.data_ptr(), _stream_ptr(device))
         _native.check(rc, f"iqk_dequant_rows({member}, {in_features}x{out_features}, [{row_start}, +{rows}))")
         return out
     fn = lib.iqk_dequant_floor if floor else lib.iqk_dequant
-    rc = fn(mid, in_features, out_features, num_experts, ptrs, len(streams),
+    rc = fn(mid, in_features, out_features, num_experts, ptrs, n_streams,
             slot_ptr, int(n_slots), out.data_ptr(), _stream_ptr(device))
     _native.check(rc, f"iqk_dequant{'_floor' if floor else ''}({member}, {in_features}x{out_features})")
     return out
@@ -412,7 +438,7 @@ def fused_matmul(member: str, x: torch.Tensor, streams: list[torch.Tensor], num_
     rows = out_features - row_start if rows is None else int(rows)
     if row_start < 0 or rows <= 0 or row_start + rows > out_features:
         raise IqkKernelError(f"row range [{row_start}, {row_start + rows}) is outside out_features {out_features}")
-    device = check_streams(member, streams, num_experts, out_features, n)
+    device, ptrs, n_streams = _streams_for(member, streams, num_experts, out_features, n)
     _require_cuda(x, "x", torch.float16, device)
     _require_cuda(group_offsets, "group_offsets", (torch.int32, torch.uint32), device)
     _require_cuda(x_rows, "x_rows", (torch.int32, torch.uint32), device)
@@ -429,9 +455,8 @@ def fused_matmul(member: str, x: torch.Tensor, streams: list[torch.Tensor], num_
         _require_cuda(out, "out", torch.float16, device)
         if tuple(out.shape) != (P, rows):
             raise IqkKernelError(f"out must be {(P, rows)}")
-    ptrs = _native.pointer_array([t.data_ptr() for t in streams])
     rc = _native.load().iqk_fused_gemm(
-        _native.MEMBER_IDS[member], n, out_features, num_experts, x.data_ptr(), int(x.shape[0]), ptrs, len(streams),
+        _native.MEMBER_IDS[member], n, out_features, num_experts, x.data_ptr(), int(x.shape[0]), ptrs, n_streams,
         row_start, rows, group_offsets.data_ptr(), x_rows.data_ptr(), y_rows.data_ptr() if y_rows is not None else None, P,
         out.data_ptr(), _stream_ptr(device))
     _native.check(rc, f"iqk_fused_gemm({member}, {n}x{out_features}, P={P})")
@@ -442,6 +467,6 @@ __all__ = [
     "DEQUANT_THREADS", "IQ2_MEMBERS", "MEMBERS", "ROWS_PER_TG",
     "SUPPORTED_IN_FEATURES", "TABLE_INPUT_NAMES", "WEIGHTS_PER_LANE", "IqkKernelError",
     "check_dequant_geometry", "check_gemv_geometry", "check_streams", "dequant", "dequant_input_names",
-    "FUSED_MEMBERS", "ROUTE_MAX_EXPERTS", "check_iq2_member", "fused_fits", "fused_matmul", "gemv", "pack", "route", "stream_floor", "gemv_input_names", "gemv_sorted", "grouped_gemm",
+    "CheckedStreams", "FUSED_MEMBERS", "ROUTE_MAX_EXPERTS", "check_iq2_member", "fused_fits", "fused_matmul", "gemv", "pack", "route", "stream_floor", "gemv_input_names", "gemv_sorted", "grouped_gemm",
     "stream_dtypes",
 ]

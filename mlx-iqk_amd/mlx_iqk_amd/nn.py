@@ -98,6 +98,26 @@ class IqkSwitchLinear(torch.nn.Module):
         dtypes = stream_dtypes(member)
         for name, shape in component_shapes(member, num_experts, out_features, in_features).items():
             self.register_buffer(name, torch.zeros(shape, dtype=dtypes[name], device=device))
+        # the streams checked once for the launchers (kernels.CheckedStreams),
+        # dropped whenever a stream is reassigned or the module moves
+        object.__setattr__(self, "_stream_set", frozenset(self.stream_names()))
+        object.__setattr__(self, "_checked_streams", None)
+
+    def __setattr__(self, name, value):
+        if name in self.__dict__.get("_stream_set", ()):
+            object.__setattr__(self, "_checked_streams", None)
+        super().__setattr__(name, value)
+
+    def _apply(self, fn, *args, **kwargs):
+        object.__setattr__(self, "_checked_streams", None)
+        return super()._apply(fn, *args, **kwargs)
+
+    def _checked(self) -> kernels.CheckedStreams:
+        """The streams as the launchers take them, checked on first use."""
+        if self._checked_streams is None:
+            object.__setattr__(self, "_checked_streams", kernels.CheckedStreams(
+                self.member, self._streams(), self.num_experts, self.out_features, self.in_features))
+        return self._checked_streams
 
     # -- wire streams -------------------------------------------------------
 
@@ -155,12 +175,12 @@ class IqkSwitchLinear(torch.nn.Module):
     def dequantized(self) -> torch.Tensor:
         """Full fp16 dequantization ``[E, out, in]``, bit-identical to the CPU decode
         (reference: src/mlx_iqk/nn.py:155-169)."""
-        return kernels.dequant(self.member, self._streams(), self.num_experts, self.out_features,
+        return kernels.dequant(self.member, self._checked(), self.num_experts, self.out_features,
                                self.in_features)
 
     def dequantized_experts(self, slot_of_expert: torch.Tensor, n_slots: int) -> torch.Tensor:
         """fp16 ``[n_slots, out, in]`` holding expert ``e`` in slot ``slot_of_expert[e]``."""
-        return kernels.dequant(self.member, self._streams(), self.num_experts, self.out_features,
+        return kernels.dequant(self.member, self._checked(), self.num_experts, self.out_features,
                                self.in_features, slot_of_expert=slot_of_expert, n_slots=n_slots)
 
     def dequantized_range(self, start: int, rows: int) -> torch.Tensor:
@@ -170,7 +190,7 @@ class IqkSwitchLinear(torch.nn.Module):
         buffers bound the fp16 memory a sorted prefill holds at once."""
         start, rows = int(start), int(rows)
         self._check_range(start, rows)
-        return kernels.dequant(self.member, self._streams(), self.num_experts, self.out_features,
+        return kernels.dequant(self.member, self._checked(), self.num_experts, self.out_features,
                                self.in_features, row_start=start, rows=rows)
 
     def _check_range(self, start: int, rows: int) -> None:
@@ -199,7 +219,7 @@ class IqkSwitchLinear(torch.nn.Module):
             raise IqkRuntimeError(
                 f"{mats} token-expert pairs do not tile {rows} activation row(s); "
                 "the operand and the routing disagree")
-        out = kernels.gemv(self.member, xt, self._streams(), sel, mats // rows, self.num_experts,
+        out = kernels.gemv(self.member, xt, self._checked(), sel, mats // rows, self.num_experts,
                            self.out_features)
         return out.reshape(list(indices.shape) + [self.out_features]).unsqueeze(-2)
 
@@ -213,7 +233,7 @@ class IqkSwitchLinear(torch.nn.Module):
         members only.
         """
         xt, sel, tok = self._sorted_operands(x, sorted_ids, toks)
-        return kernels.gemv_sorted(self.member, xt, self._streams(), sel, tok, self.num_experts,
+        return kernels.gemv_sorted(self.member, xt, self._checked(), sel, tok, self.num_experts,
                                    self.out_features)
 
     def gemv_union(self, x: torch.Tensor, sorted_ids: torch.Tensor, toks: torch.Tensor) -> torch.Tensor:
@@ -225,7 +245,7 @@ class IqkSwitchLinear(torch.nn.Module):
         expert's rows through L2.  The caller applies the inverse
         permutation."""
         xt, sel, tok = self._sorted_operands(x, sorted_ids, toks)
-        return kernels.gemv_sorted(self.member, xt, self._streams(), sel, tok, self.num_experts,
+        return kernels.gemv_sorted(self.member, xt, self._checked(), sel, tok, self.num_experts,
                                    self.out_features, union=True)
 
     def _device_ids(self, indices: torch.Tensor) -> torch.Tensor:
@@ -280,7 +300,7 @@ class IqkSwitchLinear(torch.nn.Module):
         offsets, x_rows, y_rows = self._route(tuple(xb.shape[:-2]), batch, indices, M, xflat.shape[0])
         if self.fused_prefill and self.member in kernels.FUSED_MEMBERS and kernels.fused_fits(
                 xflat.shape[0], self.in_features, self.out_features):
-            y = kernels.fused_matmul(self.member, xflat, self._streams(), E, self.out_features, offsets, x_rows,
+            y = kernels.fused_matmul(self.member, xflat, self._checked(), E, self.out_features, offsets, x_rows,
                                      y_rows, row_start=start, rows=rows)
             return y.reshape(tuple(batch) + (M, rows))
         # The producer route: experts are routed only if some pair names them;
@@ -293,7 +313,7 @@ class IqkSwitchLinear(torch.nn.Module):
         slot_offsets = torch.full((n_slots + 2,), P * M, dtype=torch.int32, device=device)
         slot_offsets.scatter_(0, torch.where(present, slot_of_expert, n_slots + 1).to(torch.int64), offsets[:-1])
         slot_offsets = slot_offsets[:n_slots + 1].contiguous()
-        w = kernels.dequant(self.member, self._streams(), E, self.out_features, self.in_features,
+        w = kernels.dequant(self.member, self._checked(), E, self.out_features, self.in_features,
                             slot_of_expert=slot_of_expert, n_slots=n_slots, row_start=start, rows=rows)
         y = kernels.grouped_gemm(xflat, w, slot_offsets, x_rows, y_rows)
         return y.reshape(tuple(batch) + (M, rows))

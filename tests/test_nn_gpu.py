@@ -189,6 +189,28 @@ def test_the_two_routes_agree_on_the_same_dispatch(device, member):
 
 
 @pytest.mark.parametrize("member", fmt.MEMBERS)
+def test_reloaded_streams_are_the_ones_used(device, member):
+    """The module checks its streams once for the launchers; reloading them
+    (new tensors at new addresses) makes the next call use the new weights on
+    both routes."""
+    n = 2048
+    module, ref_a = _module(member, n, 71, device)
+    wire_b = wirepack.random_wire(member, EXPERTS * OUT, n, seed=72, scales="serving")
+    shapes = fmt.component_shapes(member, EXPERTS, OUT, n)
+    ref_b = oracle.dequantize(member, wire_b, n).reshape(EXPERTS, OUT, n)
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((4, 1, 1, n)).astype(np.float16)
+    idx = np.stack([rng.choice(EXPERTS, 3, replace=False) for _ in range(4)]).astype(np.int64)
+    xt, it = torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device)
+    want = lambda ref: np.einsum("tn,tkon->tko", x[:, 0, 0].astype(np.float64), ref[idx].astype(np.float64))
+    for sorted_ in (False, True):
+        assert _rel(module(xt, it, sorted_indices=sorted_)[..., 0, :], want(ref_a)) < 3e-3
+    module.load_streams({k: np.ascontiguousarray(v).reshape(shapes[k]) for k, v in fmt.pack(member, wire_b, n).items()})
+    for sorted_ in (False, True):
+        assert _rel(module(xt, it, sorted_indices=sorted_)[..., 0, :], want(ref_b)) < 3e-3
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
 def test_gemv_refuses_a_pair_count_that_does_not_tile_the_rows(device, member):
     module, _ = _module(member, 2048, 61, device)
     x = torch.zeros((3, 1, 1, 2048), dtype=torch.float16, device=device)
