@@ -404,16 +404,28 @@ def prefill_cell(torch, device, args, seed: int):
         # each kernel timed over `burst` back-to-back dispatches (steady state, as
         # a prefill's projections run), rounds alternating the routes
         reps, burst = 3, 4
+        # the route is a kernel of a few microseconds: timed from a captured
+        # graph of `burst` calls, so the figure is the kernel's, not the
+        # launches' host time
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            kernels.route(ids, EXPERTS, 1, 1, flat.size)
+        torch.cuda.current_stream().wait_stream(side)
+        route_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(route_graph):
+            for _ in range(burst):
+                kernels.route(ids, EXPERTS, 1, 1, flat.size)
         times = {"producer": [], "floor": [], "gemm": [], "fused": [], "route": []}
         for _ in range(reps):
             for key in ("producer", "floor", "gemm", "fused", "route"):
                 a, b = ev(), ev()
                 a.record()
-                for _ in range(burst):
+                for _ in range(1 if key == "route" else burst):
                     if key == "gemm":
                         kernels.grouped_gemm(xin.reshape(-1, n), w, offs, rows, out=yg)
                     elif key == "route":
-                        kernels.route(ids, EXPERTS, 1, 1, flat.size)
+                        route_graph.replay()
                     elif key == "fused":
                         kernels.fused_matmul(member, xin.reshape(-1, n), mod._streams(), EXPERTS, out, offs_e, rows,
                                              out=yf)
