@@ -199,15 +199,15 @@ constexpr bool kMaskedA = MEMBER != IQ2_K && R == 1;
 
 // Shared memory of one workgroup: the activations' three byte planes (and a
 // zero span when every lane reads A), 2^-E per 32-element block, the
-// wavefronts' partial row sums (32 R rows), and for IQ1_S_R4 the expanded
-// grid and each block's integer 2 sum(f).
-template <int MEMBER, int N, int R>
+// wavefronts' partial row sums (32 R rows of each of its P pairs), and for
+// IQ1_S_R4 the expanded grid and each block's integer 2 sum(f).
+template <int MEMBER, int N, int R, int P>
 struct Gemv2Smem {
     static constexpr bool IQ1 = MEMBER == IQ1_S_R4;
     uint8_t dig[3 * kPlaneStride<N> + (kMaskedA<MEMBER, R> ? 0 : Gemv2Shape<MEMBER, N>::WK)] __attribute__((aligned(16)));
     float sbs[N / 32] __attribute__((aligned(16)));
     float nsbs[MEMBER == IQ2_KS ? N / 32 : 4] __attribute__((aligned(16)));  // -16 x 2^-E (IQ2_KS)
-    float part[Gemv2Shape<MEMBER, N>::KS][4][kGroupRows * R];
+    float part[P][Gemv2Shape<MEMBER, N>::KS][4][kGroupRows * R];
     int fsum[IQ1 ? N / 32 : 4] __attribute__((aligned(16)));
     uint2_t b8[IQ1 ? IQK_IQ1S_GRID_SIZE : 1];
     uint2_t ktab[MEMBER == IQ2_K ? 32 : 1];
@@ -739,7 +739,7 @@ void gemv_mfma_kernel(Gemv2Args a) {
     using S = Gemv2Shape<MEMBER, N>;
     constexpr int KS = S::KS;
     constexpr int ROWS = kGroupRows * R;  // rows per workgroup
-    __shared__ Gemv2Smem<MEMBER, N, R> sm;
+    __shared__ Gemv2Smem<MEMBER, N, R, 1> sm;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, l = tid & 63;
@@ -837,38 +837,183 @@ void gemv_mfma_kernel(Gemv2Args a) {
         // Partials of the row's lanes and wavefronts: wave 0 sums them after
         // the barrier.
 #pragma unroll
-        for (int r = 0; r < R; ++r) sm.part[kq][g][16 * (R * tile + r) + n] = acc[r];
+        for (int r = 0; r < R; ++r) sm.part[0][kq][g][16 * (R * tile + r) + n] = acc[r];
         __syncthreads();
         if (tid < ROWS) {
             float sum = 0.f;
 #pragma unroll
             for (int k = 0; k < KS; ++k)
-                sum += (sm.part[k][0][tid] + sm.part[k][1][tid]) + (sm.part[k][2][tid] + sm.part[k][3][tid]);
+                sum += (sm.part[0][k][0][tid] + sm.part[0][k][1][tid]) + (sm.part[0][k][2][tid] + sm.part[0][k][3][tid]);
             a.y[size_t(m0) * a.out_features + rowg + tid] = valid && x_ok ? uint16_t(float_to_half_bits(sum)) : kHalfNaN;
         }
     }
 }
 
-template <int MEMBER, int FLOOR, int MODE, int R>
+// P consecutive pairs of one activation row (pairs mode, one row block a
+// wavefront; P = 1 is gemv_mfma_kernel): the workgroup stages the
+// activations once and serves the same 32 rows of each pair's expert in
+// turn, so the staging's VALU work (a quarter of a single pair's) is shared
+// P ways.  That pays in dispatches of many tokens, where back-to-back
+// workgroups are bound by VALU issue rather than by HBM.
+template <int MEMBER, int N, int FLOOR, int P>
+__global__ __launch_bounds__((Gemv2Shape<MEMBER, N>::THREADS))
+__attribute__((amdgpu_waves_per_eu(6)))
+void gemv_mfma_pairs_kernel(Gemv2Args a) {
+    using S = Gemv2Shape<MEMBER, N>;
+    constexpr int KS = S::KS;
+    constexpr int ROWS = kGroupRows;  // rows per workgroup
+    __shared__ Gemv2Smem<MEMBER, N, 1, P> sm;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, l = tid & 63;
+    const int n = l & 15, g = l >> 4;
+    const int kq = wave % KS, tile = wave / KS;
+    // pairs m0 .. m0 + P - 1, all reading activation row blockIdx.z
+    const uint32_t m0 = blockIdx.z * a.pairs_per_row + blockIdx.y * P;
+    const uint32_t rowg = blockIdx.x * ROWS;
+
+    // Activation (and IQ1_S_R4 grid) loads first: they do not wait for the
+    // expert id, and vector loads retire in order, so staging them waits for
+    // none of the stream bytes issued after them.
+    const bool stager = tid < S::UNITS;  // uniform per wavefront
+    uint4_t xv = {0u, 0u, 0u, 0u};         // fp16 pairs 4tid .. 4tid+3 of the pair's row
+    if (stager) xv = load_u4(bytes(a.x) + (blockIdx.z * (2 * N) + 16 * uint32_t(tid)));
+    constexpr bool IQ1 = MEMBER == IQ1_S_R4;
+    // IQ1_S_R4: the codes of grid entries 4tid .. 4tid+3
+    constexpr bool GRID = IQ1 && FLOOR != kFloor;
+    static_assert(!IQ1 || IQK_IQ1S_GRID_SIZE == 4 * S::THREADS, "four grid entries per thread");
+    uint2_t gridc = {0u, 0u};
+    if constexpr (GRID) gridc = reinterpret_cast<const uint2_t *>(iqk_iq1s_grid_codes)[tid];
+    constexpr bool KTAB = MEMBER == IQ2_K && FLOOR == kDecode;
+    uint2_t ktv = {0u, 0u};
+    if (KTAB && tid < 32) ktv = reinterpret_cast<const uint2_t *>(kIq2kTab.w)[tid];
+
+    // An id beyond the stack reads expert 0 (in bounds) and writes NaN rows.
+    // No early exit: a branch here would let the compiler sink the loads
+    // above behind the wait for the id.
+    uint32_t e[P];
+    bool valid[P];  // uniform per workgroup
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const uint32_t e_raw = a.sel[m0 + p];
+        valid[p] = e_raw < a.num_experts;
+        e[p] = valid[p] ? e_raw : 0u;
+    }
+    using Lane = LaneOf<MEMBER, N>;
+    // this wavefront's 16 rows of pair p's expert
+    const auto row_of = [&](int p) { return e[p] * a.out_features + rowg + 16 * tile + n; };
+    Lane lane[1];
+    lane[0].load(a, row_of(0), kq, g);
+
+    if constexpr (GRID) {  // the grid expanded to int8 in LDS, once for all P pairs
+        uint4_t g0, g1;
+        expand_grid_pair(gridc.x, g0);
+        expand_grid_pair(gridc.y, g1);
+        reinterpret_cast<uint4_t *>(sm.b8)[2 * tid] = g0;
+        reinterpret_cast<uint4_t *>(sm.b8)[2 * tid + 1] = g1;
+    }
+    if constexpr (FLOOR == kDecode) {
+        if (KTAB && tid < 32) sm.ktab[tid] = ktv;
+        if (stager)
+            stage_activations<N, !IQ1, !kMaskedA<MEMBER, 1>, kExpBlock<MEMBER>, S::WK>(
+                sm.dig, sm.sbs, MEMBER == IQ2_KS ? sm.nsbs : nullptr, IQ1 ? sm.fsum : nullptr,
+                MEMBER == IQ2_K ? sm.fw : nullptr, tid, xv);
+    }
+    if constexpr (FLOOR == kDecode || GRID) __syncthreads();
+    const int ai = l & 15;  // this lane's A row
+    const bool data = (ai >> 2) == g && (ai & 3) < 3;
+    constexpr bool MASKED = kMaskedA<MEMBER, 1>;
+    constexpr int LANE_K = IQ1 ? 128 : 64;
+    const uint8_t *abase = sm.dig + (data || MASKED ? (ai & 3) * kPlaneStride<N> + S::WK * kq + LANE_K * g
+                                                    : 3 * kPlaneStride<N>);
+    const bool reads = data || !MASKED;  // lanes that read A
+    const float *sbs = sm.sbs + (S::WK / 32) * kq;
+
+    // Each pair's contraction in turn, straight-line code; its partial row
+    // sums (of the row's lanes and wavefronts) meet in LDS.  A pair's stream
+    // loads go out once the previous pair's decode is done with its registers:
+    // loading them a pair ahead needs ~100 VGPRs, four wavefronts per SIMD
+    // instead of six, and measured slower.
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        if (p > 0) lane[0].load(a, row_of(p), kq, g);
+        float acc[1];
+        if constexpr (FLOOR != kDecode) {
+            uint32_t h = xv.x + 3u * xv.y + 5u * xv.z + 7u * xv.w + lane[0].hash();
+            if constexpr (GRID) h += lane[0].grid_hash(sm.b8);  // kFloorGrid: every lookup of the decode
+            acc[0] = float(h & 0xffu);
+        } else if constexpr (IQ1) {
+            Lane::template decode<1, true>(lane, abase, reads, sbs, sm.fsum + (S::WK / 32) * kq, sm.b8, g, acc);
+        } else if constexpr (MEMBER == IQ2_KS) {
+            Lane::template decode<1, true>(lane, abase, reads, sbs, sm.nsbs + (S::WK / 32) * kq, g, acc);
+        } else {
+            Lane::template decode<1, true>(lane, abase, sm.sbs + (S::WK / 64) * kq, sm.fw + (S::WK / 16) * kq,
+                                           sm.ktab, g, acc);
+        }
+        // the row index again from an opaque copy of the thread index: held
+        // across the decode it costs a register the decode needs
+        int t2 = tid;
+        asm volatile("" : "+v"(t2));
+        sm.part[p][(t2 >> 6) % KS][(t2 >> 4) & 3][16 * ((t2 >> 6) / KS) + (t2 & 15)] = acc[0];
+    }
+    // The first P x 32 threads sum the partials after the barrier.
+    __syncthreads();
+    if (tid < ROWS * P) {
+        const int p = tid / ROWS, row = tid % ROWS;
+        float sum = 0.f;
+#pragma unroll
+        for (int k = 0; k < KS; ++k)
+            sum += (sm.part[p][k][0][row] + sm.part[p][k][1][row]) + (sm.part[p][k][2][row] + sm.part[p][k][3][row]);
+        bool ok = true;
+#pragma unroll
+        for (int q = 0; q < P; ++q)
+            if (q == p) ok = ok && valid[q];
+        a.y[size_t(m0 + uint32_t(p)) * a.out_features + rowg + uint32_t(row)] =
+            ok ? uint16_t(float_to_half_bits(sum)) : kHalfNaN;
+    }
+}
+
+template <int MEMBER, int FLOOR, int MODE, int R, int P>
 int launch_gemv_mfma(int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t st) {
     const uint32_t groups = a.out_features / (kGroupRows * R);
-    const dim3 grid = MODE == kPairs ? dim3{groups, a.pairs_per_row, mats / a.pairs_per_row} : dim3{groups, 1u, mats};
+    const dim3 grid = MODE == kPairs ? dim3{groups, a.pairs_per_row / P, mats / a.pairs_per_row} : dim3{groups, 1u, mats};
     const dim3 block4096{uint32_t(Gemv2Shape<MEMBER, 4096>::THREADS)}, block2048{uint32_t(Gemv2Shape<MEMBER, 2048>::THREADS)};
-    if (n == 4096)
+    static_assert(P == 1 || (MODE == kPairs && R == 1), "several pairs a workgroup: pairs mode, one row block");
+    if constexpr (P > 1) {
+        if (n == 4096)
+            hipLaunchKernelGGL((gemv_mfma_pairs_kernel<MEMBER, 4096, FLOOR, P>), grid, block4096, 0, st, a);
+        else
+            hipLaunchKernelGGL((gemv_mfma_pairs_kernel<MEMBER, 2048, FLOOR, P>), grid, block2048, 0, st, a);
+    } else if (n == 4096) {
         hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 4096, FLOOR, MODE, R>), grid, block4096, 0, st, a);
-    else
+    } else {
         hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 2048, FLOOR, MODE, R>), grid, block2048, 0, st, a);
+    }
     return record_launch(hipGetLastError());
 }
 
-template <int FLOOR, int MODE, int R>
+template <int FLOOR, int MODE, int R, int P = 1>
 int launch_member(int member, int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t st) {
     switch (member) {
-        case IQK_MEMBER_IQ2_KS: return launch_gemv_mfma<IQ2_KS, FLOOR, MODE, R>(n, a, mats, st);
-        case IQK_MEMBER_IQ2_K: return launch_gemv_mfma<IQ2_K, FLOOR, MODE, R>(n, a, mats, st);
+        case IQK_MEMBER_IQ2_KS: return launch_gemv_mfma<IQ2_KS, FLOOR, MODE, R, P>(n, a, mats, st);
+        case IQK_MEMBER_IQ2_K: return launch_gemv_mfma<IQ2_K, FLOOR, MODE, R, P>(n, a, mats, st);
         default:
-            if constexpr (MODE == kPairs) return launch_gemv_mfma<IQ1_S_R4, FLOOR, MODE, R>(n, a, mats, st);
+            if constexpr (MODE == kPairs) return launch_gemv_mfma<IQ1_S_R4, FLOOR, MODE, R, P>(n, a, mats, st);
             return IQK_ERR_MEMBER;  // no sorted or union form for IQ1_S_R4
+    }
+}
+
+// A decode launch in pairs mode: R row blocks a wavefront, P pairs a workgroup.
+template <int FLOOR, int R>
+int launch_pairs(int member, int64_t n, const Gemv2Args &a, uint32_t mats, int pairs, hipStream_t st) {
+    if constexpr (R != 1) {
+        return launch_member<FLOOR, kPairs, R, 1>(member, n, a, mats, st);
+    } else {
+        switch (pairs) {
+            case 3: return launch_member<FLOOR, kPairs, 1, 3>(member, n, a, mats, st);
+            case 2: return launch_member<FLOOR, kPairs, 1, 2>(member, n, a, mats, st);
+            default: return launch_member<FLOOR, kPairs, 1, 1>(member, n, a, mats, st);
+        }
     }
 }
 
@@ -881,6 +1026,19 @@ int launch_member(int member, int64_t n, const Gemv2Args &a, uint32_t mats, hipS
 // slower with two).
 constexpr uint64_t kTwoRowMinGroups = 2 * 768;
 constexpr uint64_t kTwoRowMinGroupsIq2 = 8 * 768;
+
+// Pairs a workgroup (pairs mode, one row block a wavefront): three pairs of
+// one activation row share its staging once a dispatch has two rounds of the
+// chip's 768 resident workgroups.  Measured (256 experts, top-6 gate and up
+// as one dispatch, back to back): IQ2_K 48.7 -> 45.7 us at 8 tokens, 188 ->
+// 176-178 us at 32, 13.9 -> 13.3 us at 2; IQ2_KS 44.8 -> 42.5 us at 8.  Six
+// pairs a workgroup measured the same or slower.
+constexpr uint64_t kSharedStagingMinGroups = 2 * 768;
+
+int pairs_per_group(uint64_t workgroups, uint32_t pairs_per_row) {
+    if (workgroups < kSharedStagingMinGroups) return 1;
+    return pairs_per_row % 3 == 0 ? 3 : pairs_per_row % 2 == 0 ? 2 : 1;
+}
 
 // Called by the GEMV entry points (after their argument checks) when
 // out_features is a multiple of the workgroup's 32 rows; returns -1 when this
@@ -916,17 +1074,18 @@ int gemv_mfma_dispatch(int floor, int member, int64_t n, int64_t out, int64_t nu
                                                         : n == 2048 && groups >= kTwoRowMinGroupsIq2);
         // only IQ1_S_R4 has grid lookups to keep; the others' kFloorGrid is kFloor
         const int kind = floor == kFloorGrid && member != IQK_MEMBER_IQ1_S_R4 ? kFloor : floor;
+        const int pairs = two ? 1 : pairs_per_group(groups, pairs_per_row);
         if (two) {
             switch (kind) {
-                case kFloor: return launch_member<kFloor, kPairs, 2>(member, n, a, mats, st);
-                case kFloorGrid: return launch_member<kFloorGrid, kPairs, 2>(member, n, a, mats, st);
-                default: return launch_member<kDecode, kPairs, 2>(member, n, a, mats, st);
+                case kFloor: return launch_pairs<kFloor, 2>(member, n, a, mats, pairs, st);
+                case kFloorGrid: return launch_pairs<kFloorGrid, 2>(member, n, a, mats, pairs, st);
+                default: return launch_pairs<kDecode, 2>(member, n, a, mats, pairs, st);
             }
         }
         switch (kind) {
-            case kFloor: return launch_member<kFloor, kPairs, 1>(member, n, a, mats, st);
-            case kFloorGrid: return launch_member<kFloorGrid, kPairs, 1>(member, n, a, mats, st);
-            default: return launch_member<kDecode, kPairs, 1>(member, n, a, mats, st);
+            case kFloor: return launch_pairs<kFloor, 1>(member, n, a, mats, pairs, st);
+            case kFloorGrid: return launch_pairs<kFloorGrid, 1>(member, n, a, mats, pairs, st);
+            default: return launch_pairs<kDecode, 1>(member, n, a, mats, pairs, st);
         }
     }
     if (floor != kDecode) return IQK_ERR_ARGUMENT;

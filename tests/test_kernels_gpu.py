@@ -141,15 +141,19 @@ def test_gemv_matches_a_float64_reference_per_pair_rows(device, member, n):
 
 @pytest.mark.parametrize("member", fmt.MEMBERS)
 @pytest.mark.parametrize("n", kernels.SUPPORTED_IN_FEATURES)
-def test_gemv_large_dispatch_equals_small_dispatches(device, member, n):
+@pytest.mark.parametrize("top_k", (3, 2))
+def test_gemv_large_dispatch_equals_small_dispatches(device, member, n, top_k):
     """A large dispatch takes two 16-row blocks per wavefront (shared
     activation reads): IQ1_S_R4 from 2 x 768 row workgroups, the IQ2 members at
-    2048 wide from 8 x 768.  A row's arithmetic is the same, so its outputs
-    equal those of the same pairs in small one-block dispatches bit for bit,
-    and meet the float64 gate.  The IQ2 members' 4096-wide dispatches (one
-    block at any size) and their sorted form are held to the same."""
-    print(f"gemv large dispatch {member} n={n}", flush=True)
-    out, tokens, top_k = 256, 256, 3  # 768 pairs x 8 row workgroups = 6144
+    2048 wide from 8 x 768.  Otherwise, from 2 x 768 row workgroups, one
+    workgroup serves three (top-3) or two (top-2) pairs of a token, staging
+    its activations once.  A row's arithmetic is the same, so its outputs
+    equal those of the same pairs in small dispatches (one block, one pair a
+    workgroup) bit for bit, and meet the float64 gate; an invalid id or an
+    infinite activation turns only its own pairs' rows NaN.  The IQ2 members'
+    sorted form is held to the same, and the large dispatch's floor runs."""
+    print(f"gemv large dispatch {member} n={n} top_k={top_k}", flush=True)
+    out, tokens = 256, 256  # 256 top_k pairs x 8 row workgroups: 6144 (top-3), 4096 (top-2)
     _, streams, ref = _case(member, n, wirepack.seed_for(member, n, "large"), device, out=out)
     rng = np.random.default_rng(23)
     x = rng.standard_normal((tokens, n)).astype(np.float16)
@@ -162,7 +166,7 @@ def test_gemv_large_dispatch_equals_small_dispatches(device, member, n):
     nan_pairs[70 * top_k:71 * top_k] = True
     xt, st = torch.from_numpy(x).to(device), torch.from_numpy(sel).to(device)
     big = kernels.gemv(member, xt, streams, st, top_k, EXPERTS, out).cpu().numpy()
-    chunk = 32  # 96 pairs x 8 = 768 row workgroups a call
+    chunk = 32  # at most 96 pairs x 8 = 768 row workgroups a call
     small = np.concatenate([kernels.gemv(member, xt[t:t + chunk], streams, st[t * top_k:(t + chunk) * top_k], top_k,
                                          EXPERTS, out).cpu().numpy() for t in range(0, tokens, chunk)])
     assert np.array_equal(big.view(np.uint16), small.view(np.uint16)), member
@@ -177,6 +181,9 @@ def test_gemv_large_dispatch_equals_small_dispatches(device, member, n):
         ys = kernels.gemv_sorted(member, xt, streams, st[torch.from_numpy(order).to(device)], toks, EXPERTS,
                                  out).cpu().numpy()
         assert np.array_equal(ys.view(np.uint16), big[order].view(np.uint16)), member
+    yf = kernels.gemv(member, xt, streams, st, top_k, EXPERTS, out, floor=True).float().cpu().numpy()
+    assert yf.shape == big.shape
+    assert np.all(np.isnan(yf[sel >= EXPERTS])) and np.all(np.isfinite(yf[sel < EXPERTS])), member
 
 
 @pytest.mark.parametrize("n", kernels.SUPPORTED_IN_FEATURES)
