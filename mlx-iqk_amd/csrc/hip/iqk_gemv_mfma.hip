@@ -174,8 +174,10 @@ __device__ __forceinline__ int4_t mfma(int4_t a, int4_t b, int4_t c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// The A operands of K MFMAs, 16 bytes each from p.  Only lanes that carry
-// activations read LDS; the others keep the zeros they start with.
+// The A operands of K MFMAs, 16 bytes each from p, read by the lanes with
+// `data`.  The decodes pass `data` true for their first read, where the lanes
+// that carry no activations point at a zero span: they keep those zeros for
+// the rest of the kernel (no zeroing instructions, no later reads).
 template <int K>
 __device__ __forceinline__ void read_a(int4_t (&a)[K], const uint8_t *p, bool data) {
     if (data) {
@@ -197,6 +199,11 @@ __device__ __forceinline__ int4_t read_a_all(const uint8_t *p) {
 template <int MEMBER, int R>
 constexpr bool kMaskedA = MEMBER != IQ2_K && R == 1;
 
+// Bytes of zeros after the byte planes: a wavefront's whole span when every
+// lane reads A, else the 64 bytes of a lane's first read.
+template <int MEMBER, int N, int R>
+constexpr int kZeroSpan = kMaskedA<MEMBER, R> ? 64 : Gemv2Shape<MEMBER, N>::WK;
+
 // Shared memory of one workgroup: the activations' three byte planes (and a
 // zero span when every lane reads A), 2^-E per 32-element block, the
 // wavefronts' partial row sums (32 R rows of each of its P pairs), and for
@@ -204,7 +211,7 @@ constexpr bool kMaskedA = MEMBER != IQ2_K && R == 1;
 template <int MEMBER, int N, int R, int P>
 struct Gemv2Smem {
     static constexpr bool IQ1 = MEMBER == IQ1_S_R4;
-    uint8_t dig[3 * kPlaneStride<N> + (kMaskedA<MEMBER, R> ? 0 : Gemv2Shape<MEMBER, N>::WK)] __attribute__((aligned(16)));
+    uint8_t dig[3 * kPlaneStride<N> + kZeroSpan<MEMBER, N, R>] __attribute__((aligned(16)));
     float sbs[N / 32] __attribute__((aligned(16)));
     float nsbs[MEMBER == IQ2_KS ? N / 32 : 4] __attribute__((aligned(16)));  // -16 x 2^-E (IQ2_KS)
     float part[P][Gemv2Shape<MEMBER, N>::KS][4][kGroupRows * R];
@@ -232,14 +239,13 @@ constexpr int kExpBlock = MEMBER == IQ2_K ? 64 : 32;
 // One exponent E covers BLOCK (32 or 64) consecutive elements, 2^-E lands in
 // sbs[element / BLOCK] (and -16 x 2^-E in nsbs, when given).  With `fsum`,
 // each 32-element block's 2 sum(f) lands there too, with `fword` each
-// 16-element word's sum(f); with ZERO_SPAN, the WK bytes
-// after the planes are cleared.
-template <int N, bool TRANSPOSED, bool ZERO_SPAN, int BLOCK, int WK>
+// 16-element word's sum(f); the ZERO_BYTES after the planes are cleared.
+template <int N, bool TRANSPOSED, int ZERO_BYTES, int BLOCK>
 __device__ __forceinline__ void stage_activations(uint8_t *dig, float *sbs, float *nsbs, int *fsum, float *fword, int tid,
                                                   uint4_t xv) {
     static_assert(BLOCK == 32 || BLOCK == 64, "4 or 8 threads per exponent block");
     const uint32_t wd = uint32_t(tid) >> 1, hp = uint32_t(tid) & 1u;
-    if (ZERO_SPAN && tid < WK / 16)
+    if (tid < ZERO_BYTES / 16)
         *reinterpret_cast<uint4_t *>(dig + 3 * kPlaneStride<N> + 16 * tid) = uint4_t{0u, 0u, 0u, 0u};
     uint32_t xp[4] = {xv.x, xv.y, xv.z, xv.w};
     if constexpr (TRANSPOSED) {  // hp 0 keeps pairs 0, 2 and takes 4, 6; hp 1 keeps 5, 7 and takes 1, 3
@@ -393,7 +399,7 @@ struct LaneIq2ks {
             int4_t D[R][2];
             if (s < 4) {
                 if constexpr (!EARLY) prep(s);
-                read_a(A, abase + 256 * s, data);
+                read_a(A, abase + 256 * s, data || s == 0);
 #pragma unroll
                 for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -674,7 +680,7 @@ struct LaneIq1s {
                 const int i = c >> 2, b = c & 3;
                 if ((b & 1) == 0) {  // blocks b, b+1
                     if constexpr (!EARLY) prep(i, b >> 1);
-                    read_a(A, abase + 512 * i + 32 * b, data);
+                    read_a(A, abase + 512 * i + 32 * b, data || c == 0);
                 }
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
@@ -809,7 +815,7 @@ void gemv_mfma_kernel(Gemv2Args a) {
                 if (KTAB && tid < 32) sm.ktab[tid] = ktv;
             }
             if (stager)
-                stage_activations<N, !IQ1, !kMaskedA<MEMBER, R>, kExpBlock<MEMBER>, S::WK>(
+                stage_activations<N, !IQ1, kZeroSpan<MEMBER, N, R>, kExpBlock<MEMBER>>(
                     sm.dig, sm.sbs, MEMBER == IQ2_KS ? sm.nsbs : nullptr, IQ1 ? sm.fsum : nullptr,
                     MEMBER == IQ2_K ? sm.fw : nullptr, tid, xv);
             __syncthreads();
@@ -817,8 +823,8 @@ void gemv_mfma_kernel(Gemv2Args a) {
             const bool data = (ai >> 2) == g && (ai & 3) < 3;
             constexpr bool MASKED = kMaskedA<MEMBER, R>;
             constexpr int LANE_K = IQ1 ? 128 : 64;
-            const uint8_t *abase = sm.dig + (data || MASKED ? (ai & 3) * kPlaneStride<N> + S::WK * kq + LANE_K * g
-                                                            : 3 * kPlaneStride<N>);
+            const uint8_t *abase = sm.dig + (data ? (ai & 3) * kPlaneStride<N> + S::WK * kq + LANE_K * g
+                                                  : 3 * kPlaneStride<N>);
             const bool reads = data || !MASKED;  // lanes that read A
             const float *sbs = sm.sbs + (S::WK / 32) * kq;
             using Lane = LaneOf<MEMBER, N>;
@@ -915,7 +921,7 @@ void gemv_mfma_pairs_kernel(Gemv2Args a) {
     if constexpr (FLOOR == kDecode) {
         if (KTAB && tid < 32) sm.ktab[tid] = ktv;
         if (stager)
-            stage_activations<N, !IQ1, !kMaskedA<MEMBER, 1>, kExpBlock<MEMBER>, S::WK>(
+            stage_activations<N, !IQ1, kZeroSpan<MEMBER, N, 1>, kExpBlock<MEMBER>>(
                 sm.dig, sm.sbs, MEMBER == IQ2_KS ? sm.nsbs : nullptr, IQ1 ? sm.fsum : nullptr,
                 MEMBER == IQ2_K ? sm.fw : nullptr, tid, xv);
     }
@@ -924,8 +930,8 @@ void gemv_mfma_pairs_kernel(Gemv2Args a) {
     const bool data = (ai >> 2) == g && (ai & 3) < 3;
     constexpr bool MASKED = kMaskedA<MEMBER, 1>;
     constexpr int LANE_K = IQ1 ? 128 : 64;
-    const uint8_t *abase = sm.dig + (data || MASKED ? (ai & 3) * kPlaneStride<N> + S::WK * kq + LANE_K * g
-                                                    : 3 * kPlaneStride<N>);
+    const uint8_t *abase = sm.dig + (data ? (ai & 3) * kPlaneStride<N> + S::WK * kq + LANE_K * g
+                                          : 3 * kPlaneStride<N>);
     const bool reads = data || !MASKED;  // lanes that read A
     const float *sbs = sm.sbs + (S::WK / 32) * kq;
 
