@@ -79,7 +79,6 @@ struct Gemv2Args {
 constexpr uint32_t kV8Base = 0x1101F3E1u;   // int8 -31, -13, 1, 17
 constexpr uint32_t kV8Shift = 0x1606F8E6u;  // int8 -26, -8, 6, 22
 constexpr uint32_t kG8Plus = 0x000901F9u;   // int8 8(g + 1/8), g = -1, 0, 1
-constexpr uint32_t kG8Minus = 0x0007FFF7u;  // int8 8(g - 1/8)
 constexpr int kWaveK = 1024;                // reduction elements per wavefront (default)
 constexpr int kGroupRows = 32;              // rows per workgroup
 
