@@ -20,7 +20,8 @@ reference's CPU dequantizer + float32 matmul on a bounded sample of the
 headline step.
 
 Protocol (reference: bench/price.py): validation before timing; decode and
-floor arms alternated with the order reversed each round; each arm is a
+floor arms alternated with the order reversed each round, each arm's round
+the best of four replays of its graph, medians over five rounds; each arm is a
 captured graph of back-to-back dispatches whose routing variants are disjoint
 chunks of expert permutations, so an expert's bytes are re-read only after
 more than 1 GB of other traffic (beyond the 256 MB MALL).  The stream arm
@@ -77,6 +78,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--rounds", type=int, default=5, help="alternated decode/floor rounds per cell")
     ap.add_argument("--block", type=int, default=200, help="dispatches per captured graph in a cell")
+    ap.add_argument("--blocks", type=int, default=4, help="graph replays per arm and round; the best one counts")
     ap.add_argument("--distinct", type=int, default=2, help="distinct quantized experts per projection")
     ap.add_argument("--cells", default="iq2_ks,iq2_k,iq1_s_r4,dequant,prefill,pack,verify,quantize",
                     help="cells after the headline ('headline' alone: the IQ2_KS cell and the headline only)")
@@ -122,14 +124,17 @@ class Arm:
         return start.elapsed_time(end) * 1e3 / self.count
 
 
-def alternate(arms: dict, rounds: int) -> dict:
+def alternate(arms: dict, rounds: int, blocks: int) -> dict:
+    """Each round times every arm as the best of `blocks` graph replays, the
+    arms in turn, the order reversed on odd rounds (bench/price.py:263-273,
+    312-340: best of 4 blocks a round, median over the rounds)."""
     names = list(arms)
     for a in arms.values():
         a.time()  # one untimed replay each
     runs = {n: [] for n in names}
     for r in range(rounds):
         for n in (names if r % 2 == 0 else names[::-1]):
-            runs[n].append(arms[n].time())
+            runs[n].append(min(arms[n].time() for _ in range(blocks)))
     return {n: {"median_us": round(statistics.median(v), 3), "min_us": round(min(v), 3),
                 "max_us": round(max(v), 3), "runs_us": [round(x, 3) for x in v]} for n, v in runs.items()}
 
@@ -247,7 +252,7 @@ def decode_cell(torch, device, member: str, tokens: int, args, seed: int, want_s
             arms["stream"] = Arm(torch, [windows.launcher(nbytes, i) for i in range(B)], "stream")
         if member == "iq1_s_r4":
             arms["floor_grid"] = Arm(torch, [launch(i, "grid") for i in range(B)], "floor_grid")
-        res = alternate(arms, args.rounds)
+        res = alternate(arms, args.rounds, args.blocks)
         res["bytes_per_dispatch"] = nbytes
         for arm in arms:
             res[arm]["gb_per_s"] = round(nbytes / (res[arm]["median_us"] * 1e-6) / 1e9, 1)
@@ -331,7 +336,7 @@ def dequant_cell(torch, device, member: str, args, seed: int):
         arms = {"decode": Arm(torch, [launch(i) for i in range(B)], "decode"),
                 "floor": Arm(torch, [launch(i, True) for i in range(B)], "floor"),
                 "range": Arm(torch, [launch_range(i) for i in range(B)], "range")}
-        r = alternate(arms, args.rounds)
+        r = alternate(arms, args.rounds, args.blocks)
         read = chunk * out * fmt.ik_row_bytes(member, n)
         written = chunk * out * n * 2
         r["range"]["rows"] = [r0, r0 + nr]
@@ -541,7 +546,7 @@ def verify_cell(torch, device, args, seed: int):
                                                union=mode == "union", out=v["y"])
         arms = {mode: Arm(torch, [launch(i, mode) for i in range(variants)], mode)
                 for mode in ("pairs", "floor", "sorted", "union")}
-        r = alternate(arms, args.rounds)
+        r = alternate(arms, args.rounds, args.blocks)
         distinct = statistics.mean(v["distinct"] for v in V)
         nbytes = distinct * out * rb
         cell = {"pairs": tokens * TOP_K, "distinct_experts_mean": round(distinct, 1),
