@@ -141,8 +141,8 @@ def test_single_iq2_ks_expert_quantized_from_seed_0(device):
 
 def test_iq2_k_routed_decode_8_tokens(device):
     """IQ2_K, 256 experts, 8 tokens x top-6 unsorted: gate [2048 x 4096] (48
-    pairs, 3072 one-block workgroups) and down [4096 x 2048] (48 pairs, 6144
-    workgroups: the two-row-block form)."""
+    pairs x 64 row groups = 3072: three pairs of a token a workgroup) and down
+    [4096 x 2048] (48 pairs, 6144 row workgroups: the two-row-block form)."""
     _decode_case(device, "iq2_k", 8, seed=303)
 
 
@@ -159,11 +159,15 @@ def test_iq2_ks_routed_decode_1_token(device):
     _decode_case(device, "iq2_ks", 1, seed=202)
 
 
-def test_decode_is_deterministic(device):
-    """The same dispatch twice: identical fp16 bits (no atomics, fixed order)."""
-    module, _ = _stack("iq2_k", *DN, wirepack.seed_for("config", "iq2_k", "down"), device)
+@pytest.mark.parametrize("which", ("gate", "down"))
+def test_decode_is_deterministic(device, which):
+    """The same dispatch twice: identical fp16 bits (no atomics, fixed order),
+    for the gate (three pairs a workgroup) and the down (two row blocks)."""
+    geo = GU if which == "gate" else DN
+    module, _ = _stack("iq2_k", *geo, wirepack.seed_for("config", "iq2_k", which), device)
     rng = np.random.default_rng(5)
-    x = torch.from_numpy(rng.standard_normal((8, TOP_K, 1, DN[1])).astype(np.float16)).to(device)
+    shape = (8, 1, 1, geo[1]) if which == "gate" else (8, TOP_K, 1, geo[1])
+    x = torch.from_numpy(rng.standard_normal(shape).astype(np.float16)).to(device)
     idx = torch.from_numpy(np.stack([rng.choice(E, TOP_K, replace=False) for _ in range(8)]).astype(np.int32)).to(device)
     a, b = module(x, idx), module(x, idx)
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
