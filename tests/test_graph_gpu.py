@@ -25,33 +25,38 @@ pytestmark = pytest.mark.gpu
 EXPERTS, OUT, N, TOP_K = 8, 256, 2048, 4
 
 
-def _module(member, seed, device):
-    wire = wirepack.random_wire(member, EXPERTS * OUT, N, seed=seed, scales="serving")
+def _module(member, seed, device, out=OUT):
+    wire = wirepack.random_wire(member, EXPERTS * out, N, seed=seed, scales="serving")
     streams = fmt.pack(member, wire, N)
-    shapes = fmt.component_shapes(member, EXPERTS, OUT, N)
-    module = IqkSwitchLinear(member, EXPERTS, OUT, N, device=device)
+    shapes = fmt.component_shapes(member, EXPERTS, out, N)
+    module = IqkSwitchLinear(member, EXPERTS, out, N, device=device)
     module.load_streams({k: np.ascontiguousarray(v).reshape(shapes[k]) for k, v in streams.items()})
     return module
 
 
-def _routing(rng, tokens):
-    return np.stack([rng.choice(EXPERTS, TOP_K, replace=False) for _ in range(tokens)]).astype(np.int64)
+def _routing(rng, tokens, top_k=TOP_K):
+    return np.stack([rng.choice(EXPERTS, top_k, replace=False) for _ in range(tokens)]).astype(np.int64)
 
 
 @pytest.mark.parametrize("member", fmt.MEMBERS)
-@pytest.mark.parametrize("route", ["decode", "fused", "producer"])
+@pytest.mark.parametrize("route", ["decode", "decode_three_pairs", "fused", "producer"])
 def test_forward_replays_from_a_graph(device, member, route):
-    module = _module(member, 41, device)
+    """decode: 1 token x top-4 (4 pairs, one pair a workgroup); decode_three_pairs:
+    21 tokens x top-3 over 1024 rows (63 pairs x 32 row groups = 2016, where the
+    IQ2 members serve three pairs of a token a workgroup); fused and producer:
+    24 tokens x top-4 (96 pairs take the prefill route)."""
+    three = route == "decode_three_pairs"
+    module = _module(member, 41, device, out=1024 if three else OUT)
     module.fused_prefill = route != "producer"
-    tokens = 1 if route == "decode" else 24  # 4 pairs take the decode route, 96 the prefill route
-    prefill = route != "decode"
+    tokens, top_k = (21, 3) if three else (1 if route == "decode" else 24, TOP_K)
+    prefill = route in ("fused", "producer")
     rng = np.random.default_rng(5)
     x = torch.empty(tokens, 1, 1, N, dtype=torch.float16, device=device)
-    idx = torch.empty(tokens, TOP_K, dtype=torch.int64, device=device)
+    idx = torch.empty(tokens, top_k, dtype=torch.int64, device=device)
 
     def fill():
         x.copy_(torch.from_numpy(rng.standard_normal((tokens, 1, 1, N)).astype(np.float16)))
-        idx.copy_(torch.from_numpy(_routing(rng, tokens)))
+        idx.copy_(torch.from_numpy(_routing(rng, tokens, top_k)))
 
     def run():
         return module(x, idx, sorted_indices=prefill)
