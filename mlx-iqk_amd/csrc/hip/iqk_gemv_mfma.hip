@@ -38,11 +38,11 @@
 //   and zero elsewhere, so D rows 4g..4g+2 -- which the MFMA places in lane
 //   group g -- collect exactly that lane's weights, one byte plane each:
 //   sum(w x) = 2^-E (D0 + 2^8 D1 + 2^16 D2).  Each lane folds its own
-//   (row, sub-block) sums with the sub-block's scale.  Only the 12 lanes
-//   whose A row carries activations read LDS; the others hold zeros in
-//   registers for the whole kernel (IQ2_K, and the two-block form below:
-//   every lane reads, the others from a zero span).  The partial sums of a
-//   row's lanes and wavefronts meet in LDS.
+//   (row, sub-block) sums with the sub-block's scale.  Every lane reads its
+//   A operands from LDS, the 52 lanes whose A rows carry no activations from
+//   a zero span (reading only in the 12 data lanes, behind a branch, with
+//   zeros held in registers, measured 0.3-2% slower at 1 token).  The
+//   partial sums of a row's lanes and wavefronts meet in LDS.
 // * Two row blocks.  Large IQ1_S_R4 dispatches give each wavefront 32 rows
 //   (two 16-row blocks, R = 2) that share every A read, so a workgroup
 //   stages its activations once for 64 rows; the per-row arithmetic is the
@@ -147,9 +147,9 @@ __device__ __forceinline__ int digits_sum(int4_t d) { return (((d.z << 8) + d.y)
 __device__ __forceinline__ uint32_t lo16_x8(uint32_t v) { return (v & 0xffffu) << 3; }
 __device__ __forceinline__ uint32_t hi16_x8(uint32_t v) { return (v >> 16) << 3; }
 
-// Keeps a value computed where it stands.  The masked A reads split a decode
-// into one block per super-block, and without a use in its own block each
-// fold would be sunk behind the last stream word, into every wavefront's tail.
+// Keeps a value computed where it stands: without a use in its own
+// super-block each fold could be sunk behind the last stream word, into every
+// wavefront's tail.
 __device__ __forceinline__ void pin(float &v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void pin(uint32_t &v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void pin(int &v) { asm volatile("" : "+v"(v)); }
@@ -173,16 +173,12 @@ __device__ __forceinline__ int4_t mfma(int4_t a, int4_t b, int4_t c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// The A operands of K MFMAs, 16 bytes each from p, read by the lanes with
-// `data`.  The decodes pass `data` true for their first read, where the lanes
-// that carry no activations point at a zero span: they keep those zeros for
-// the rest of the kernel (no zeroing instructions, no later reads).
+// The A operands of K MFMAs, 16 bytes each from p (lanes without
+// activations point into a zero span).
 template <int K>
-__device__ __forceinline__ void read_a(int4_t (&a)[K], const uint8_t *p, bool data) {
-    if (data) {
+__device__ __forceinline__ void read_a(int4_t (&a)[K], const uint8_t *p) {
 #pragma unroll
-        for (int j = 0; j < K; ++j) a[j] = __builtin_bit_cast(int4_t, *reinterpret_cast<const uint4_t *>(p + 16 * j));
-    }
+    for (int j = 0; j < K; ++j) a[j] = __builtin_bit_cast(int4_t, *reinterpret_cast<const uint4_t *>(p + 16 * j));
 }
 
 // One A operand read by every lane (non-data lanes point into a zero span).
@@ -190,27 +186,19 @@ __device__ __forceinline__ int4_t read_a_all(const uint8_t *p) {
     return __builtin_bit_cast(int4_t, *reinterpret_cast<const uint4_t *>(p));
 }
 
-// Whether a member's kernel reads A only in the data lanes (fewer LDS bytes,
-// more live registers: the other lanes hold zeros for the whole kernel) or in
-// every lane, the others from a zero span.  IQ2_K, with a fold per 16
-// weights, is register-bound and reads in every lane, and so does every
-// member at two row blocks per wavefront, where each read serves both.
-template <int MEMBER, int R>
-constexpr bool kMaskedA = MEMBER != IQ2_K && R == 1;
+// Bytes of zeros after the byte planes: a wavefront's reduction span, what a
+// lane without activations reads.
+template <int MEMBER, int N>
+constexpr int kZeroSpan = Gemv2Shape<MEMBER, N>::WK;
 
-// Bytes of zeros after the byte planes: a wavefront's whole span when every
-// lane reads A, else the 64 bytes of a lane's first read.
-template <int MEMBER, int N, int R>
-constexpr int kZeroSpan = kMaskedA<MEMBER, R> ? 64 : Gemv2Shape<MEMBER, N>::WK;
-
-// Shared memory of one workgroup: the activations' three byte planes (and a
-// zero span when every lane reads A), 2^-E per 32-element block, the
+// Shared memory of one workgroup: the activations' three byte planes and a
+// zero span, 2^-E per 32-element block, the
 // wavefronts' partial row sums (32 R rows of each of its P pairs), and for
 // IQ1_S_R4 the expanded grid and each block's integer 2 sum(f).
 template <int MEMBER, int N, int R, int P>
 struct Gemv2Smem {
     static constexpr bool IQ1 = MEMBER == IQ1_S_R4;
-    uint8_t dig[3 * kPlaneStride<N> + kZeroSpan<MEMBER, N, R>] __attribute__((aligned(16)));
+    uint8_t dig[3 * kPlaneStride<N> + kZeroSpan<MEMBER, N>] __attribute__((aligned(16)));
     float sbs[N / 32] __attribute__((aligned(16)));
     float nsbs[MEMBER == IQ2_KS ? N / 32 : 4] __attribute__((aligned(16)));  // -16 x 2^-E (IQ2_KS)
     float part[P][Gemv2Shape<MEMBER, N>::KS][4][kGroupRows * R];
@@ -345,8 +333,8 @@ struct LaneIq2ks {
     // lane instance each, which share every A read; sbs / nsbs: 2^-E and
     // -16 x 2^-E of each 32-element block.
     template <int R, bool EARLY>
-    __device__ __forceinline__ static void decode(const LaneIq2ks (&ln)[R], const uint8_t *abase, bool data,
-                                                  const float *sbs, const float *nsbs, int g, float (&out)[R]) {
+    __device__ __forceinline__ static void decode(const LaneIq2ks (&ln)[R], const uint8_t *abase, const float *sbs,
+                                                  const float *nsbs, int g, float (&out)[R]) {
         // Scale index x 2^-E and alphabet pool of sub-blocks 8s+2g+h, formed
         // from the scale bytes alone (left to the scheduler: pinning them
         // here measured slower), so the code words meet only their expansion,
@@ -398,7 +386,7 @@ struct LaneIq2ks {
             int4_t D[R][2];
             if (s < 4) {
                 if constexpr (!EARLY) prep(s);
-                read_a(A, abase + 256 * s, data || s == 0);
+                read_a(A, abase + 256 * s);
 #pragma unroll
                 for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -633,9 +621,8 @@ struct LaneIq1s {
     // each 32-element block.
     // R rows, one lane instance each, share every A read.
     template <int R, bool EARLY>
-    __device__ __forceinline__ static void decode(const LaneIq1s (&ln)[R], const uint8_t *abase, bool data,
-                                                  const float *sbs, const int *fsum2, const uint2_t *b8, int g,
-                                                  float (&out)[R]) {
+    __device__ __forceinline__ static void decode(const LaneIq1s (&ln)[R], const uint8_t *abase, const float *sbs,
+                                                  const int *fsum2, const uint2_t *b8, int g, float (&out)[R]) {
         // Each block's scale x 2^-E and its negative-shift correction
         // 2 sum(f) (or 0); 2s + 1 of the two blocks of a qh dword lands in
         // its bytes 0 and 2 in two ops.  All are formed before the first
@@ -679,7 +666,7 @@ struct LaneIq1s {
                 const int i = c >> 2, b = c & 3;
                 if ((b & 1) == 0) {  // blocks b, b+1
                     if constexpr (!EARLY) prep(i, b >> 1);
-                    read_a(A, abase + 512 * i + 32 * b, data || c == 0);
+                    read_a(A, abase + 512 * i + 32 * b);
                 }
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
@@ -814,17 +801,15 @@ void gemv_mfma_kernel(Gemv2Args a) {
                 if (KTAB && tid < 32) sm.ktab[tid] = ktv;
             }
             if (stager)
-                stage_activations<N, !IQ1, kZeroSpan<MEMBER, N, R>, kExpBlock<MEMBER>>(
+                stage_activations<N, !IQ1, kZeroSpan<MEMBER, N>, kExpBlock<MEMBER>>(
                     sm.dig, sm.sbs, MEMBER == IQ2_KS ? sm.nsbs : nullptr, IQ1 ? sm.fsum : nullptr,
                     MEMBER == IQ2_K ? sm.fw : nullptr, tid, xv);
             __syncthreads();
             const int ai = l & 15;  // this lane's A row
             const bool data = (ai >> 2) == g && (ai & 3) < 3;
-            constexpr bool MASKED = kMaskedA<MEMBER, R>;
             constexpr int LANE_K = IQ1 ? 128 : 64;
             const uint8_t *abase = sm.dig + (data ? (ai & 3) * kPlaneStride<N> + S::WK * kq + LANE_K * g
                                                   : 3 * kPlaneStride<N>);
-            const bool reads = data || !MASKED;  // lanes that read A
             const float *sbs = sm.sbs + (S::WK / 32) * kq;
             using Lane = LaneOf<MEMBER, N>;
             // the prologue of every super-block before the first code word,
@@ -832,9 +817,9 @@ void gemv_mfma_kernel(Gemv2Args a) {
             // wavefront per SIMD
             constexpr bool EARLY = R == 1;
             if constexpr (IQ1)
-                Lane::template decode<R, EARLY>(lane, abase, reads, sbs, sm.fsum + (S::WK / 32) * kq, sm.b8, g, acc);
+                Lane::template decode<R, EARLY>(lane, abase, sbs, sm.fsum + (S::WK / 32) * kq, sm.b8, g, acc);
             else if constexpr (MEMBER == IQ2_KS)
-                Lane::template decode<R, EARLY>(lane, abase, reads, sbs, sm.nsbs + (S::WK / 32) * kq, g, acc);
+                Lane::template decode<R, EARLY>(lane, abase, sbs, sm.nsbs + (S::WK / 32) * kq, g, acc);
             else
                 Lane::template decode<R, EARLY>(lane, abase, sm.sbs + (S::WK / 64) * kq, sm.fw + (S::WK / 16) * kq,
                                          sm.ktab, g, acc);
@@ -920,18 +905,16 @@ void gemv_mfma_pairs_kernel(Gemv2Args a) {
     if constexpr (FLOOR == kDecode) {
         if (KTAB && tid < 32) sm.ktab[tid] = ktv;
         if (stager)
-            stage_activations<N, !IQ1, kZeroSpan<MEMBER, N, 1>, kExpBlock<MEMBER>>(
+            stage_activations<N, !IQ1, kZeroSpan<MEMBER, N>, kExpBlock<MEMBER>>(
                 sm.dig, sm.sbs, MEMBER == IQ2_KS ? sm.nsbs : nullptr, IQ1 ? sm.fsum : nullptr,
                 MEMBER == IQ2_K ? sm.fw : nullptr, tid, xv);
     }
     if constexpr (FLOOR == kDecode || GRID) __syncthreads();
     const int ai = l & 15;  // this lane's A row
     const bool data = (ai >> 2) == g && (ai & 3) < 3;
-    constexpr bool MASKED = kMaskedA<MEMBER, 1>;
     constexpr int LANE_K = IQ1 ? 128 : 64;
     const uint8_t *abase = sm.dig + (data ? (ai & 3) * kPlaneStride<N> + S::WK * kq + LANE_K * g
                                           : 3 * kPlaneStride<N>);
-    const bool reads = data || !MASKED;  // lanes that read A
     const float *sbs = sm.sbs + (S::WK / 32) * kq;
 
     // Each pair's contraction in turn, straight-line code; its partial row
@@ -948,9 +931,9 @@ void gemv_mfma_pairs_kernel(Gemv2Args a) {
             if constexpr (GRID) h += lane[0].grid_hash(sm.b8);  // kFloorGrid: every lookup of the decode
             acc[0] = float(h & 0xffu);
         } else if constexpr (IQ1) {
-            Lane::template decode<1, true>(lane, abase, reads, sbs, sm.fsum + (S::WK / 32) * kq, sm.b8, g, acc);
+            Lane::template decode<1, true>(lane, abase, sbs, sm.fsum + (S::WK / 32) * kq, sm.b8, g, acc);
         } else if constexpr (MEMBER == IQ2_KS) {
-            Lane::template decode<1, true>(lane, abase, reads, sbs, sm.nsbs + (S::WK / 32) * kq, g, acc);
+            Lane::template decode<1, true>(lane, abase, sbs, sm.nsbs + (S::WK / 32) * kq, g, acc);
         } else {
             Lane::template decode<1, true>(lane, abase, sm.sbs + (S::WK / 64) * kq, sm.fw + (S::WK / 16) * kq,
                                            sm.ktab, g, acc);
