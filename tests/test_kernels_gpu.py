@@ -186,6 +186,36 @@ def test_gemv_large_dispatch_equals_small_dispatches(device, member, n, top_k):
     assert np.all(np.isnan(yf[sel >= EXPERTS])) and np.all(np.isfinite(yf[sel < EXPERTS])), member
 
 
+@pytest.mark.parametrize("case", range(8))
+def test_gemv_dispatch_forms_agree_on_random_shapes(device, case):
+    """Seeded random geometry and routing: member, width, 256-512 rows, 2-8
+    experts, 1-8 pairs a token (ids repeat where a token has more pairs than
+    the stack has experts), and tokens enough for 1536-8000 row
+    workgroups, so the dispatch takes the large-dispatch forms (three or two
+    pairs a workgroup, or two row blocks) wherever their thresholds are met.
+    It equals the same pairs dispatched a token at a time (one pair a
+    workgroup, one row block) bit for bit, and meets the float64 gate."""
+    rng = np.random.default_rng(wirepack.seed_for("forms", case))
+    member = fmt.MEMBERS[case % 3]
+    n = kernels.SUPPORTED_IN_FEATURES[(case // 3) % 2]
+    out = 32 * int(rng.integers(8, 17))
+    experts = int(rng.integers(2, 9))
+    top_k = (7, 6, 5, 1, 4, 2, 3, 8)[case]  # three, two and one pair a workgroup
+    groups_per_token = top_k * out // 32
+    tokens = -(-int(rng.integers(1536, 8000)) // groups_per_token)
+    print(f"gemv forms {member} n={n} out={out} experts={experts} top_k={top_k} tokens={tokens}", flush=True)
+    _, streams, ref = _case(member, n, wirepack.seed_for("forms", member, n, case), device, experts=experts, out=out)
+    x = rng.standard_normal((tokens, n)).astype(np.float16)
+    sel = np.concatenate([rng.permutation(experts)[:top_k] if top_k <= experts
+                          else rng.integers(0, experts, size=top_k) for _ in range(tokens)]).astype(np.int32)
+    xt, st = torch.from_numpy(x).to(device), torch.from_numpy(sel).to(device)
+    big = kernels.gemv(member, xt, streams, st, top_k, experts, out).cpu().numpy()
+    small = np.concatenate([kernels.gemv(member, xt[t:t + 1], streams, st[t * top_k:(t + 1) * top_k], top_k,
+                                         experts, out).cpu().numpy() for t in range(tokens)])
+    assert np.array_equal(big.view(np.uint16), small.view(np.uint16)), (member, n, out, top_k, tokens)
+    _check_gemv(big, oracle.gemv_reference(ref, sel, x, top_k), (member, n, out, top_k))
+
+
 @pytest.mark.parametrize("n", kernels.SUPPORTED_IN_FEATURES)
 @pytest.mark.parametrize("out", (16, 48, 192))
 def test_gemv_iq2_ks_tiles(device, n, out):
