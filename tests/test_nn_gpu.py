@@ -536,8 +536,9 @@ def test_fused_prefill_experts_of_many_tiles(device, member, n):
     """Experts that span several 64-slot M-tiles, full and partial: sizes 300
     (four full tiles and a 44-slot one), 128 (two full), 200 (three full and
     an 8-slot one), 129 (two full and a one-slot one), 64, 5, 1 and 0.  Both
-    routes meet the float64 gate and agree with each other, and row ranges
-    concatenate to the unsplit call bit for bit."""
+    routes meet the float64 gate and agree with each other, a second fused
+    call repeats the first bit for bit, and row ranges concatenate to the
+    unsplit call bit for bit."""
     print(f"fused prefill many tiles {member} n={n}", flush=True)
     module, ref = _module(member, n, wirepack.seed_for(member, n, "wide"), device)
     sizes = [300, 128, 200, 1, 0, 5, 64, 129]
@@ -551,6 +552,7 @@ def test_fused_prefill_experts_of_many_tiles(device, member, n):
     assert _rel(fused, want) < 3e-3 and _rel(producer, want) < 3e-3
     diff = (fused.float() - producer.float()).abs().max().item()
     assert diff <= 2e-3 * producer.float().abs().max().item()
+    assert np.array_equal(_bits(module(xt, it, sorted_indices=True)), _bits(fused))
     half = OUT // 2
     parts = torch.cat([module.sorted_matmul_range(xt, it, 0, half),
                        module.sorted_matmul_range(xt, it, half, half)], dim=-1)
