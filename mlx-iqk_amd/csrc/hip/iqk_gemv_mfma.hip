@@ -43,10 +43,15 @@
 //   a zero span (reading only in the 12 data lanes, behind a branch, with
 //   zeros held in registers, measured 0.3-2% slower at 1 token).  The
 //   partial sums of a row's lanes and wavefronts meet in LDS.
-// * Two row blocks.  Large IQ1_S_R4 dispatches give each wavefront 32 rows
-//   (two 16-row blocks, R = 2) that share every A read, so a workgroup
-//   stages its activations once for 64 rows; the per-row arithmetic is the
-//   same as with one block, so results are identical bit for bit.
+// * Two row blocks.  Large IQ1_S_R4 dispatches, and the IQ2 members' large
+//   2048-wide ones, give each wavefront 32 rows (two 16-row blocks, R = 2)
+//   that share every A read, so a workgroup stages its activations once for
+//   64 rows; the per-row arithmetic is the same as with one block, so
+//   results are identical bit for bit.
+// * Several pairs a workgroup.  Other large dispatches in pairs mode serve
+//   three (or two) consecutive pairs of one activation row in one workgroup
+//   (gemv_mfma_pairs_kernel): the activations are staged once for the
+//   pairs' experts, again with each row's arithmetic unchanged.
 //
 // The floor variants keep every global load and delete the decode.
 
