@@ -331,9 +331,9 @@ void fused_gemm_kernel(FusedArgs a) {
     // side had every store phase hit each bank twice).  Byte offsets into x
     // are 32-bit (the entry point refuses an x of 4 GiB or more).
     // A row past the tile's last slot feeds only MFMA rows that are never
-    // stored, so IQ1_S_R4 neither loads nor stages it (its LDS row keeps
-    // whatever it held): a partial tile (most tiles of a skewed routing)
-    // stages only its slots.  Measured on the 2048-token Zipf prefill:
+    // stored, so IQ1_S_R4 neither loads nor stages it per step (its LDS row
+    // keeps the zeros written at the tile's start): a partial tile (most
+    // tiles of a skewed routing) stages only its slots.  Measured on the 2048-token Zipf prefill:
     // IQ1_S_R4 -4%; the IQ2 members, whose step the branch splits for the
     // scheduler, +1 to +2%, so they stage every row.
     const int xrow_l = tid / kXChunks, xchunk = tid % kXChunks;
@@ -365,15 +365,35 @@ void fused_gemm_kernel(FusedArgs a) {
             if (xlive[i]) v[i] = load_u4(xbase + xoff[i] + uint32_t(2 * kFusedKS * s));
     };
     // Each 8-element chunk is stored in the order (0,4,1,5,2,6,3,7), the
-    // order expand_word_paired gives the weights.
+    // order expand_word_paired gives the weights.  A row past the tile's last
+    // slot is staged as zeros, so the MFMAs of those rows multiply zeros: the
+    // kernel is bound by the clock its power allows, and zero operands draw
+    // less (IQ2_KS gate 400.7 -> 392.5 us, IQ2_K gate 426.7 -> 417.0 us on
+    // the 2048-token Zipf prefill; the rows were a dead slot's real data).
+    // The IQ2 members stage every row, the dead ones through v_perm
+    // selectors of 0x0c bytes (which give zero bytes: no instruction added);
+    // IQ1_S_R4 zeroes its dead rows in both buffers once.
+    uint32_t xsel_lo[kXPer], xsel_hi[kXPer];
+#pragma unroll
+    for (int i = 0; i < kXPer; ++i) {
+        const bool dead = m0 + uint32_t(xrow_l + kXRows * i) >= gend;
+        xsel_lo[i] = dead ? 0x0c0c0c0cu : 0x05040100u;
+        xsel_hi[i] = dead ? 0x0c0c0c0cu : 0x07060302u;
+        if (IQ1 && dead) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+                *reinterpret_cast<uint4_t *>(xs[b] + (xrow_l + kXRows * i) * kXStride + 16 * xchunk) =
+                    uint4_t{0u, 0u, 0u, 0u};
+        }
+    }
     const auto store_x = [&](int buf, const uint4_t *v) {
         uint8_t *dst = xs[buf] + xrow_l * kXStride + 16 * xchunk;
 #pragma unroll
         for (int i = 0; i < kXPer; ++i)
             if (xlive[i])
                 *reinterpret_cast<uint4_t *>(dst + kXRows * kXStride * i) =
-                    uint4_t{perm(v[i].z, v[i].x, 0x05040100u), perm(v[i].z, v[i].x, 0x07060302u),
-                            perm(v[i].w, v[i].y, 0x05040100u), perm(v[i].w, v[i].y, 0x07060302u)};
+                    uint4_t{perm(v[i].z, v[i].x, xsel_lo[i]), perm(v[i].z, v[i].x, xsel_hi[i]),
+                            perm(v[i].w, v[i].y, xsel_lo[i]), perm(v[i].w, v[i].y, xsel_hi[i])};
     };
 
     // this lane's weight row and code words; a row past out_features reads
