@@ -7,9 +7,9 @@
 //
 // The prefill's cost is streaming the fp16 weights (16 MiB per expert
 // projection, each read once per 64-slot M-tile), so the kernel is shaped
-// for HBM: every wavefront streams its own weight rows with the next step's
-// loads in flight, and the M-tiles of one expert run on one XCD, back to
-// back, so a weight block's second and later reads come from that XCD's L2.
+// for HBM: a block keeps several steps of its weights in flight, and the
+// M-tiles of one expert run on one XCD, back to back, so a weight block's
+// second and later reads come from that XCD's L2.
 //
 // Work list.  Slots are sorted by group; a group of c slots needs ceil(c/BM)
 // M-tiles.  A first in-block scan of the group sizes counts the M-tiles T
@@ -23,16 +23,27 @@
 //
 // Tile.  512 threads, eight wavefronts, BM x BN = 64 x 256; wavefront w owns
 // weight rows 32w .. 32w+31 of the block (the columns of
-// v_mfma_f32_32x32x16_f16) for both 32-slot row blocks.  Reduction steps of
-// 64: the step's activations (64 slots x 64 fp16) are staged in LDS, double
-// buffered, one barrier a step; each lane loads its weight row's four
-// 16-byte chunks of the step straight into registers (the four loads of a
-// row's 128 bytes are consecutive instructions, so the line is fetched
-// once).  Loads run three steps ahead of the MFMAs in four rotating register
-// sets (about 150 VGPRs: one block of eight wavefronts a CU), so a CU keeps
-// three steps of weights and activations, ~120 KB, in flight.  Any out_features works: a lane's B row is its D column,
-// so columns at or beyond out_features are neither loaded nor stored.  A
-// tile with at most 32 real slots skips its second row block's MFMAs.
+// v_mfma_f32_32x32x16_f16) for both 32-slot row blocks; reduction steps of
+// 64.  A tile with at most 32 real slots skips its second row block's MFMAs.
+// Any out_features works: a lane's B row is its D column, so columns at or
+// beyond out_features read an in-bounds row and are never stored.
+//
+// Two forms of the step loop:
+// * grouped_gemm_lds_kernel (K a multiple of 64, the prefill's case): both
+//   operands go from global memory straight into LDS (16-byte
+//   global_load_lds_dwordx4), one load instruction moving 8 rows x 128
+//   contiguous bytes, so it touches 8 cache lines.  Register loads in the
+//   MFMA's layout (each lane its own weight row) touch 32 lines an
+//   instruction, and measured ~15% slower on the Zipf prefill (996 against
+//   849 us per projection) at the same bytes.  Each wavefront streams its
+//   own 32 weight rows into four 32 KiB stages (three steps ahead, no
+//   registers held), the activations go into three 8 KiB stages (two ahead),
+//   and a lane stores chunk c of its row at c ^ (row % 8), so the MFMA
+//   operand reads (8 rows a phase, one chunk each) hit distinct banks.
+// * grouped_gemm_kernel (any K a multiple of 32): register staging, the
+//   step's activations copied to LDS, the weights loaded in the MFMA's layout
+//   three steps ahead in four rotating register sets; the last step may end
+//   past K (its upper half is zeroed).
 
 #include <type_traits>
 
@@ -54,9 +65,10 @@ constexpr int kGemmAStride = 2 * kGemmBK + 16;  // LDS bytes per staged activati
 constexpr int kGemmAChunks = kGemmBK / 8;     // 16-byte activation chunks per row and step
 constexpr int kGemmARows = kGemmThreads / kGemmAChunks;  // slot rows one staging pass covers
 constexpr int kGemmAPer = kGemmBM / kGemmARows;          // staging passes (16-byte chunks a thread moves a step)
-// Register sets per operand: loads run kGemmStages - 1 steps ahead.  On the
-// 2048-token Zipf prefill (gate [2048 x 4096]) two sets measured 1113 us,
-// four 987 us; eight sets, or four of 128-wide steps, spill at 256 VGPRs.
+// Register sets per operand of grouped_gemm_kernel: loads run kGemmStages - 1
+// steps ahead (on the 2048-token Zipf prefill, gate [2048 x 4096], two sets
+// measured 1113 us, four 987 us; eight sets, or four of 128-wide steps, spill
+// at 256 VGPRs).
 constexpr int kGemmStages = 4;
 static_assert(kGemmBM % kGemmARows == 0 && kGemmThreads % kGemmAChunks == 0, "whole staging passes");
 
@@ -70,11 +82,8 @@ struct GemmArgs {
     uint32_t K, N, n_groups, n_slots, n_x_rows;
 };
 
-// FULL: K is a multiple of kGemmStages 64-wide steps, so the step loop has
-// no branch at all: loads past the last step re-read it, stages past it are
-// never read.  Otherwise the last step may end past K (its upper half is
-// zeroed) and the step count is any.
-template <bool FULL>
+// The general form: any K a multiple of 32 (the last step may end past K;
+// its upper half is zeroed) and any step count.
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void grouped_gemm_kernel(GemmArgs a) {
     __shared__ TileScan ts;
@@ -106,10 +115,8 @@ void grouped_gemm_kernel(GemmArgs a) {
     // activation staging: thread t moves 16 bytes (chunk t % C) of slot rows
     // t / C + R i a step (C chunks a row, R rows a pass, i < kGemmAPer)
     const int arow = tid / kGemmAChunks, achunk = tid % kGemmAChunks;
-    // every load below is unconditional, from an in-bounds address (a dead
-    // row reads row 0, which exists: the entry point refuses an empty x), so
-    // the loads stay straight-line code and each wait is for exactly the step
-    // it needs
+    // every load below reads an in-bounds address (a dead row reads row 0,
+    // which exists: the entry point refuses an empty x)
     const uint16_t *asrc[kGemmAPer];
 #pragma unroll
     for (int i = 0; i < kGemmAPer; ++i) {
@@ -136,14 +143,10 @@ void grouped_gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < kGemmAPer; ++i) {
             uint32_t k = s * kGemmBK;
-            if constexpr (FULL) {
-                v[i] = load_u4(asrc[i] + k);
-            } else {
-                const bool live = k + 8 * achunk < a.K;
-                k = min(k, a.K - 8 * achunk - 8);
-                const uint4_t t = load_u4(asrc[i] + k);
-                v[i] = live ? t : uint4_t{0u, 0u, 0u, 0u};
-            }
+            const bool live = k + 8 * achunk < a.K;
+            k = min(k, a.K - 8 * achunk - 8);
+            const uint4_t t = load_u4(asrc[i] + k);
+            v[i] = live ? t : uint4_t{0u, 0u, 0u, 0u};
         }
     };
     const auto store_a = [&](int buf, const AStage &v) {
@@ -165,14 +168,10 @@ void grouped_gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int u = 0; u < kGemmU; ++u) {
             uint32_t k = s * kGemmBK + 16 * u;
-            if constexpr (!FULL) {
-                const bool live = k + 8 * h < a.K;
-                k = min(k, a.K - 8 * h - 8);
-                const uint4_t v = load_u4(bsrc + k);
-                b[u] = live ? v : uint4_t{0u, 0u, 0u, 0u};
-            } else {
-                b[u] = load_u4(bsrc + k);
-            }
+            const bool live = k + 8 * h < a.K;
+            k = min(k, a.K - 8 * h - 8);
+            const uint4_t v = load_u4(bsrc + k);
+            b[u] = live ? v : uint4_t{0u, 0u, 0u, 0u};
         }
     };
 
@@ -223,7 +222,7 @@ void grouped_gemm_kernel(GemmArgs a) {
         for (uint32_t s = 0; s < ksteps; s += kGemmStages) {  // the step count and its bounds are uniform
 #pragma unroll
             for (int i = 0; i < kGemmStages; ++i) {
-                if (FULL || s + i < ksteps)
+                if (s + i < ksteps)
                     step(s + i, bq[i], bq[(i + kGemmStages - 1) % kGemmStages], aq[(i + 1) % kGemmStages],
                          aq[(i + kGemmStages - 1) % kGemmStages]);
             }
@@ -237,6 +236,167 @@ void grouped_gemm_kernel(GemmArgs a) {
     // D layout (32x32): lane l, register r holds row 8(r/4) + 4(l/32) + r%4
     // of column l % 32.
     if (!bv) return;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t dst = slot_dst[32 * mb + 8 * (r >> 2) + 4 * h + (r & 3)];
+            if (dst != kNoStore)
+                a.y[size_t(dst & 0x7fffffffu) * a.N + col] =
+                    (dst >> 31) ? uint16_t(float_to_half_bits(acc[mb][r])) : kHalfNaN;
+        }
+    }
+}
+
+
+// -- the direct-to-LDS form (K a multiple of 64) -----------------------------------
+
+// One 16-byte load per lane from global memory into LDS: lane l's 16 bytes
+// land at LDS byte lds + 16 l (M0 holds the wavefront's LDS base).  Written
+// as inline asm rather than the compiler's builtin: with the builtin every
+// __syncthreads() waits for all such loads in flight (vmcnt(0)), which would
+// drain the pipeline each step; here the waits are explicit (below) and the
+// compiler sees no load to wait for.
+__device__ __forceinline__ void load_to_lds16(uint32_t lds, const void *src) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory", "m0");
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t lds_offset(T *p) {
+    return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t *)(p)));
+}
+
+constexpr int kLdsRow = 2 * kGemmBK;              // bytes of one row's step: 128
+constexpr int kLdsBStages = 4;                     // weight loads run three steps ahead
+constexpr int kLdsAStages = 3;                     // activation loads two steps ahead
+constexpr int kLdsBStage = kGemmBN * kLdsRow;      // 32 KiB: 256 weight rows
+constexpr int kLdsAStage = kGemmBM * kLdsRow;      // 8 KiB: 64 slot rows
+constexpr int kLdsWaveRows = kGemmBN / kGemmWaves; // 32 weight rows a wavefront streams
+static_assert(kLdsRow == 128 && kGemmBM == 8 * kGemmWaves && kLdsWaveRows == 8 * kGemmU,
+              "a load instruction moves 8 rows of 128 bytes; each wavefront 8 slot rows and its 32 weight rows");
+
+// Step s of a wavefront issues A(s + 2) then B(s + 3) (1 + kGemmU loads), after
+// a prologue B(0), A(0), B(1), A(1), B(2).  Loads complete in order, so when
+// step s starts, A(s) and B(s) have landed once at most the 2 kGemmU + 1 loads
+// issued after A(s) -- B(s+1), A(s+1), B(s+2) -- are outstanding.
+static_assert(2 * kGemmU + 1 == 9, "the step's wait count below");
+
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void grouped_gemm_lds_kernel(GemmArgs a) {
+    __shared__ TileScan ts;
+    __shared__ __attribute__((aligned(16))) uint8_t bst[kLdsBStages * kLdsBStage];
+    __shared__ __attribute__((aligned(16))) uint8_t ast[kLdsAStages * kLdsAStage];
+    __shared__ uint32_t slot_dst[kGemmBM];  // as in grouped_gemm_kernel
+    constexpr uint32_t kNoStore = 0x7fffffffu;
+
+    const int tid = threadIdx.x;
+    const uint32_t ncb = (a.N + kGemmBN - 1) / kGemmBN;
+    const uint32_t tiles = count_mtiles<kGemmBM, kGemmThreads>(a.offs, a.n_groups, ts);
+    const uint32_t per_xcd = (tiles + 7) / 8;
+    const uint32_t xcd = blockIdx.x & 7u, j = blockIdx.x >> 3;
+    if (j / ncb >= per_xcd) return;  // surplus block (uniform)
+    const uint32_t tile = xcd * per_xcd + j / ncb, cblock = j % ncb;
+    if (tile >= tiles) return;
+    uint32_t g, mtile;
+    if (!find_mtile<kGemmBM, kGemmThreads>(a.offs, a.n_groups, tile, ts, g, mtile)) return;
+
+    const uint32_t gend = min(a.offs[g + 1], a.n_slots);
+    const uint32_t m0 = a.offs[g] + mtile * kGemmBM;
+    const uint32_t n0 = cblock * kGemmBN;
+    const uint32_t ksteps = a.K / kGemmBK;
+    const int wave = tid >> 6, l = tid & 63, ln = l & 31, h = l >> 5;
+
+    if (tid < kGemmBM) {  // one thread a slot: the epilogue's destination, read once
+        const uint32_t ap = m0 + uint32_t(tid);
+        uint32_t dst = kNoStore;
+        if (ap < gend) {
+            const uint32_t yrow = a.yr ? a.yr[ap] : ap;
+            if (yrow < a.n_slots) dst = yrow | (a.xr[ap] < a.n_x_rows ? 0x80000000u : 0u);
+        }
+        slot_dst[tid] = dst;
+    }
+    // A load instruction of wavefront w moves 8 rows (8 w + l / 8 of the
+    // slots, or 8 u + l / 8 of its weight rows for load u), 128 bytes each;
+    // lane l carries the row's chunk (l % 8) ^ (l / 8) into LDS position l % 8,
+    // so LDS row r holds chunk c at position c ^ (r % 8).  Dead slots and
+    // weight rows past out_features read row 0 (in bounds, never stored).
+    const uint32_t cx = 8u * (uint32_t(l & 7) ^ uint32_t(l >> 3));
+    const uint16_t *asrc;
+    {
+        const uint32_t ap = m0 + uint32_t(8 * wave + (l >> 3));
+        const uint32_t xrow = ap < gend ? a.xr[ap] : a.n_x_rows;
+        asrc = a.x + size_t(xrow < a.n_x_rows ? xrow : 0u) * a.K + cx;
+    }
+    const uint16_t *bsrc[kGemmU];
+#pragma unroll
+    for (int u = 0; u < kGemmU; ++u) {
+        const uint32_t r = n0 + uint32_t(kLdsWaveRows * wave + 8 * u + (l >> 3));
+        bsrc[u] = a.w + (size_t(g) * a.N + (r < a.N ? r : 0u)) * a.K + cx;
+    }
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t a_lds = lds_offset(ast) + wv * (8 * kLdsRow);
+    const uint32_t b_lds = lds_offset(bst) + wv * (kLdsWaveRows * kLdsRow);
+    // steps past the last re-read it into a stage nobody reads
+    const auto issue_a = [&](uint32_t s) {
+        s = min(s, ksteps - 1);
+        load_to_lds16(a_lds + (s % kLdsAStages) * kLdsAStage, asrc + s * kGemmBK);
+    };
+    const auto issue_b = [&](uint32_t s) {
+        s = min(s, ksteps - 1);
+#pragma unroll
+        for (int u = 0; u < kGemmU; ++u)
+            load_to_lds16(b_lds + (s % kLdsBStages) * kLdsBStage + 8 * kLdsRow * u, bsrc[u] + s * kGemmBK);
+    };
+    issue_b(0);
+    issue_a(0);
+    issue_b(1);
+    issue_a(1);
+    issue_b(2);
+
+    float16_t acc[2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[mb][r] = 0.f;
+
+    __syncthreads();  // the slot table
+    const uint32_t swz = 16u * uint32_t(ln & 7);  // row ln's chunk positions, as a byte xor
+    const auto run_steps = [&](auto slot_blocks) {
+        constexpr int MB = decltype(slot_blocks)::value;
+        for (uint32_t s = 0; s < ksteps; ++s) {  // the step count is uniform
+            // this wavefront's A(s) and B(s) have landed; after the barrier
+            // every wavefront's A(s) has, and every wavefront is done with
+            // step s - 1, whose stages the loads below refill
+            asm volatile("s_waitcnt vmcnt(9)\n\ts_barrier" ::: "memory");
+            issue_a(s + 2);
+            issue_b(s + 3);
+            const uint8_t *ab = ast + (s % kLdsAStages) * kLdsAStage + ln * kLdsRow;
+            const uint8_t *bb = bst + (s % kLdsBStages) * kLdsBStage + (kLdsWaveRows * wave + ln) * kLdsRow;
+#pragma unroll
+            for (int u = 0; u < kGemmU; ++u) {
+                // chunk 2u + h of the row (lanes h = l / 32 hold the MFMA's two k halves)
+                const uint32_t co = (32u * u + 16u * h) ^ swz;
+                const half8_t bf = __builtin_bit_cast(half8_t, *reinterpret_cast<const uint4_t *>(bb + co));
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    const half8_t af = __builtin_bit_cast(
+                        half8_t, *reinterpret_cast<const uint4_t *>(ab + 32 * kLdsRow * mb + co));
+                    acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc[mb], 0, 0, 0);
+                }
+            }
+        }
+    };
+    if (gend - m0 <= 32)  // uniform per block
+        run_steps(std::integral_constant<int, 1>{});
+    else
+        run_steps(std::integral_constant<int, 2>{});
+    // no load into LDS may still be in flight when the block's LDS is released
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // D layout (32x32): lane l, register r holds row 8(r/4) + 4(l/32) + r%4
+    // of column l % 32.
+    const uint32_t col = n0 + uint32_t(kLdsWaveRows * wave + ln);
+    if (col >= a.N) return;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
@@ -278,9 +438,9 @@ extern "C" int iqk_grouped_gemm(int64_t in_features, int64_t out_features, int64
     const uint64_t mtiles = (uint64_t(n_slots) + kGemmBM - 1) / kGemmBM + uint64_t(n_groups);
     const uint64_t blocks = 8 * ((mtiles + 7) / 8) * uint64_t((out_features + kGemmBN - 1) / kGemmBN);
     if (blocks > 0x7fffffffull) return IQK_ERR_ARGUMENT;
-    if (in_features % (kGemmStages * kGemmBK) == 0)
-        hipLaunchKernelGGL(grouped_gemm_kernel<true>, dim3{uint32_t(blocks)}, dim3{kGemmThreads}, 0, as_stream(stream), a);
+    if (in_features % kGemmBK == 0)
+        hipLaunchKernelGGL(grouped_gemm_lds_kernel, dim3{uint32_t(blocks)}, dim3{kGemmThreads}, 0, as_stream(stream), a);
     else
-        hipLaunchKernelGGL(grouped_gemm_kernel<false>, dim3{uint32_t(blocks)}, dim3{kGemmThreads}, 0, as_stream(stream), a);
+        hipLaunchKernelGGL(grouped_gemm_kernel, dim3{uint32_t(blocks)}, dim3{kGemmThreads}, 0, as_stream(stream), a);
     return record_launch(hipGetLastError());
 }
