@@ -38,8 +38,8 @@
 //   849 us per projection) at the same bytes.  Each wavefront streams its
 //   own 32 weight rows into four 32 KiB stages (three steps ahead, no
 //   registers held), the activations go into three 8 KiB stages (two ahead),
-//   and a lane stores chunk c of its row at c ^ (row % 8), so the MFMA
-//   operand reads (8 rows a phase, one chunk each) hit distinct banks.
+//   and a lane stores chunk c of its row at c ^ (row / 2 % 8), so the MFMA
+//   operand reads (16 rows, one chunk each) cover all 64 banks once.
 // * grouped_gemm_kernel (any K a multiple of 32): register staging, the
 //   step's activations copied to LDS, the weights loaded in the MFMA's layout
 //   three steps ahead in four rotating register sets; the last step may end
@@ -315,23 +315,23 @@ void grouped_gemm_lds_kernel(GemmArgs a) {
         }
         slot_dst[tid] = dst;
     }
-    // A load instruction of wavefront w moves 8 rows (8 w + l / 8 of the
-    // slots, or 8 u + l / 8 of its weight rows for load u), 128 bytes each;
-    // lane l carries the row's chunk (l % 8) ^ (l / 8) into LDS position l % 8,
-    // so LDS row r holds chunk c at position c ^ (r % 8).  Dead slots and
+    // A load instruction of wavefront w moves 8 rows r = 8 i + l / 8 (i = w for
+    // the slots, i = u for load u of its weight rows), 128 bytes each; lane l
+    // carries the row's chunk (l % 8) ^ (r / 2 % 8) into LDS position l % 8,
+    // so LDS row r holds chunk c at position c ^ (r / 2 % 8).  Dead slots and
     // weight rows past out_features read row 0 (in bounds, never stored).
-    const uint32_t cx = 8u * (uint32_t(l & 7) ^ uint32_t(l >> 3));
+    const auto chunk = [&](int i) { return 8u * (uint32_t(l & 7) ^ (uint32_t(4 * i + (l >> 4)) & 7u)); };
     const uint16_t *asrc;
     {
         const uint32_t ap = m0 + uint32_t(8 * wave + (l >> 3));
         const uint32_t xrow = ap < gend ? a.xr[ap] : a.n_x_rows;
-        asrc = a.x + size_t(xrow < a.n_x_rows ? xrow : 0u) * a.K + cx;
+        asrc = a.x + size_t(xrow < a.n_x_rows ? xrow : 0u) * a.K + chunk(wave);
     }
     const uint16_t *bsrc[kGemmU];
 #pragma unroll
     for (int u = 0; u < kGemmU; ++u) {
         const uint32_t r = n0 + uint32_t(kLdsWaveRows * wave + 8 * u + (l >> 3));
-        bsrc[u] = a.w + (size_t(g) * a.N + (r < a.N ? r : 0u)) * a.K + cx;
+        bsrc[u] = a.w + (size_t(g) * a.N + (r < a.N ? r : 0u)) * a.K + chunk(u);
     }
     const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
     const uint32_t a_lds = lds_offset(ast) + wv * (8 * kLdsRow);
@@ -360,7 +360,9 @@ void grouped_gemm_lds_kernel(GemmArgs a) {
         for (int r = 0; r < 16; ++r) acc[mb][r] = 0.f;
 
     __syncthreads();  // the slot table
-    const uint32_t swz = 16u * uint32_t(ln & 7);  // row ln's chunk positions, as a byte xor
+    // row ln's chunk positions, as a byte xor (rows 32 mb + ln of the slots
+    // have the same); the 16 rows of a half-wavefront's read fill all 64 banks
+    const uint32_t swz = 16u * (uint32_t(ln >> 1) & 7u);
     const auto run_steps = [&](auto slot_blocks) {
         constexpr int MB = decltype(slot_blocks)::value;
         for (uint32_t s = 0; s < ksteps; ++s) {  // the step count is uniform
