@@ -346,6 +346,32 @@ def test_grouped_gemm_is_deterministic(device):
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
+def test_grouped_gemm_addresses_operands_beyond_4gib(device):
+    """Activation rows and an expert's weights that start past 4 GiB of their
+    tensors (lane addresses are 64-bit; nothing is reduced mod 2^32).  Only the
+    rows the kernel reads are filled."""
+    print("grouped gemm beyond 4 GiB", flush=True)
+    rng = np.random.default_rng(41)
+    K, N, G, P = 4096, 65536, 9, 40
+    x_rows_total = 2 ** 19 + 64                                   # x: 4 GiB + 512 KiB
+    x = torch.empty((x_rows_total, K), dtype=torch.float16, device=device)
+    rows = (2 ** 19 + rng.permutation(64)[:P]).astype(np.int32)   # every row past byte 2^32
+    xs = rng.standard_normal((P, K)).astype(np.float16)
+    x[torch.from_numpy(rows.astype(np.int64)).to(device)] = torch.from_numpy(xs).to(device)
+    x[0] = 0  # a dead slot of the tile reads row 0
+    w = torch.empty((G, N, K), dtype=torch.float16, device=device)  # expert 8 starts at byte 2^32
+    gen = torch.Generator(device=device).manual_seed(41)
+    w[8] = (torch.randn((N, K), generator=gen, device=device) * 0.02).to(torch.float16)
+    offs = torch.tensor([0] * 9 + [P], dtype=torch.int32, device=device)
+    got = kernels.grouped_gemm(x, w, offs, torch.from_numpy(rows).to(device)).float().cpu().numpy()
+    cols = np.concatenate([np.sort(rng.choice(N, 96, replace=False)), [0, N - 1]])
+    w8 = w[8][torch.from_numpy(cols).to(device)].cpu().numpy()
+    want = xs.astype(np.float64) @ w8.astype(np.float64).T
+    rel = np.max(np.abs(got[:, cols] - want)) / np.max(np.abs(want))
+    assert rel < 3e-3, rel
+    del x, w
+
+
 # K a multiple of 64 takes the direct-to-LDS kernel (one to many steps), other K the general one
 @pytest.mark.parametrize("K,N", [(4096, 2048), (2048, 4096), (2048, 256), (2048, 32), (4096, 272), (64, 256), (192, 40),
                                  (2080, 96), (96, 288)])
