@@ -259,10 +259,17 @@ void grouped_gemm_kernel(GemmArgs a) {
 // compiler sees no load to wait for.
 // M0 is declared clobbered; no other code in these kernels uses M0 (no LDS
 // DMA builtin, message or relative register indexing), so nothing live is lost.
+// An LDS DMA that reads M0 right after an SALU write of it needs one wait
+// state on this generation (the compiler's hazard pass cannot see inside
+// inline asm, so the s_nop is written here).  The asm's only register
+// operands are the address and the LDS base; every MFMA result register of
+// the kernel is a live accumulator, so no operand can be an MFMA destination
+// still being written.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void load_to_lds16(uint32_t lds, const void *src) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
+                 : "memory", "m0");
 }
 #pragma clang diagnostic pop
 
