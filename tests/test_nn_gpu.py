@@ -414,26 +414,29 @@ def test_sorted_and_union_mark_out_of_range_rows(device, method, out):
     assert np.array_equal(_bits(got[(~bad).to(device)]), _bits(want))
 
 
-def test_union_gemv_at_the_routed_geometry(device):
-    """256 experts, gate/up geometry, the multi-token verify shape (4 tokens x
-    top-6 over few experts): bit-identical to the pair GEMV."""
-    print("union gemv routed geometry", flush=True)
-    member, E, out, n = "iq2_ks", 256, 2048, 4096
+@pytest.mark.parametrize("member", IQ2)
+def test_union_gemv_at_the_routed_geometry(device, member):
+    """256 experts, gate/up geometry, the multi-token verify shape: 8 tokens x
+    top-6 over a pool of 9 experts (long runs: most workgroups serve two
+    pairs) and over all experts (mostly one-pair workgroups); bit-identical
+    to the pair GEMV."""
+    print(f"union gemv routed geometry {member}", flush=True)
+    E, out, n = 256, 2048, 4096
     wire = wirepack.random_wire(member, E * out, n, seed=2025, scales="serving")
     shapes = fmt.component_shapes(member, E, out, n)
     module = IqkSwitchLinear(member, E, out, n, device=device)
     module.load_streams({k: np.ascontiguousarray(v).reshape(shapes[k])
                          for k, v in fmt.pack(member, wire, n).items()})
     rng = np.random.default_rng(8)
-    tokens, top_k = 4, 6
-    pool = rng.choice(E, 9, replace=False)
-    idx = np.stack([rng.choice(pool, top_k, replace=False) for _ in range(tokens)]).astype(np.int32)
-    x = torch.from_numpy(rng.standard_normal((tokens, 1, 1, n)).astype(np.float16)).to(device)
-    pair = module.gemv(x, torch.from_numpy(idx).to(device))
-    sorted_ids, toks, _order, inv = _union_operands(idx, top_k, device)
-    for fn in (module.gemv_union, module.gemv_sorted):
-        got = fn(x, sorted_ids, toks)[inv].reshape(pair.shape)
-        assert np.array_equal(_bits(got), _bits(pair))
+    tokens, top_k = 8, 6
+    for pool in (rng.choice(E, 9, replace=False), np.arange(E)):
+        idx = np.stack([rng.choice(pool, top_k, replace=False) for _ in range(tokens)]).astype(np.int32)
+        x = torch.from_numpy(rng.standard_normal((tokens, 1, 1, n)).astype(np.float16)).to(device)
+        pair = module.gemv(x, torch.from_numpy(idx).to(device))
+        sorted_ids, toks, _order, inv = _union_operands(idx, top_k, device)
+        for fn in (module.gemv_union, module.gemv_sorted):
+            got = fn(x, sorted_ids, toks)[inv].reshape(pair.shape)
+            assert np.array_equal(_bits(got), _bits(pair))
 
 
 # -- range producer and range matmul (reference: tests/test_nn.py:329-377) --
