@@ -119,10 +119,10 @@ class IqkSwitchLinear(torch.nn.Module):
                 self.member, self._streams(), self.num_experts, self.out_features, self.in_features))
         return self._checked_streams
 
-    # -- wire streams -------------------------------------------------------
+    # -- the relayout streams (module buffers) ---------------------------------
 
     def stream_names(self) -> list[str]:
-        """Relayout stream names of this member, in kernel input order."""
+        """The member's stream buffer names, ordered as the kernels take them."""
         return list(component_shapes(self.member, self.num_experts, self.out_features, self.in_features))
 
     def _streams(self) -> list[torch.Tensor]:
