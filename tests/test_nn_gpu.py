@@ -176,6 +176,36 @@ def test_prefill_marks_out_of_range_experts_with_nan(device, member, fused):
     assert np.all(np.isnan(dec[bad[:12]])) and not np.any(np.isnan(dec[~bad[:12]]))
 
 
+@pytest.mark.parametrize("fused", (True, False))
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+def test_prefill_confines_non_finite_activations_to_their_rows(device, member, fused):
+    """An inf in one token's activations and a NaN in another's make every
+    output element of those tokens' pairs non-finite (each product with the
+    inf is inf or, with a zero weight, NaN) and leave every other pair's row
+    bit for bit as in the same call on clean activations: the contraction
+    never mixes slots.  Both prefill routes."""
+    n = 2048
+    module, _ = _module(member, n, 223, device)
+    rng = np.random.default_rng(227)
+    tokens, top_k = 20, 4
+    x = rng.standard_normal((tokens, 1, 1, n)).astype(np.float16)
+    idx = rng.integers(0, EXPERTS, size=(tokens, top_k)).astype(np.int32)
+    dirty = x.copy()
+    dirty[5, 0, 0, n // 3] = np.inf
+    dirty[13, 0, 0, 7] = np.nan
+    poisoned = np.zeros((tokens, top_k), dtype=bool)
+    poisoned[[5, 13]] = True
+    module.fused_prefill = fused
+    try:
+        clean = module(torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device))
+        got = module(torch.from_numpy(dirty).to(device), torch.from_numpy(idx).to(device))
+    finally:
+        module.fused_prefill = True
+    g = got.float().cpu().numpy()
+    assert not np.any(np.isfinite(g[poisoned]))
+    assert np.array_equal(_bits(got)[~poisoned], _bits(clean)[~poisoned])
+
+
 @pytest.mark.parametrize("member", fmt.MEMBERS)
 def test_the_two_routes_agree_on_the_same_dispatch(device, member):
     n = 2048
