@@ -346,6 +346,37 @@ def test_grouped_gemm_is_deterministic(device):
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
+def test_grouped_gemm_repeats_bit_for_bit_at_the_prefill_size(device):
+    """The direct-to-LDS pipeline at the 2048-token Zipf(1.1) prefill size
+    (256 experts, [2048 x 4096], 12,288 sorted pairs): twenty back-to-back
+    calls give identical bits (its waits are written by hand, so a missing
+    one would show as calls that differ), and sampled slots match float64."""
+    from mlx_iqk_amd import synth
+    print("grouped gemm repeat at the prefill size", flush=True)
+    E, N, K = 256, 2048, 4096
+    idx = synth.zipf_routing(2048, E, 6, 1.1, 31).reshape(-1)
+    order = np.argsort(idx, kind="stable")
+    counts = np.bincount(idx, minlength=E)
+    P = idx.size
+    gen = torch.Generator(device=device).manual_seed(31)
+    w = (torch.randn((E, N, K), generator=gen, device=device) * 0.02).to(torch.float16)
+    x = torch.randn((2048, K), generator=gen, device=device).to(torch.float16)
+    offs = torch.from_numpy(np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)).to(device)
+    rows = torch.from_numpy((order // 6).astype(np.int32)).to(device)
+    first = kernels.grouped_gemm(x, w, offs, rows)
+    out = torch.empty_like(first)
+    for _ in range(20):
+        kernels.grouped_gemm(x, w, offs, rows, out=out)
+        assert torch.equal(out.view(torch.int16), first.view(torch.int16))
+    rng = np.random.default_rng(37)
+    for p in rng.choice(P, 8, replace=False):
+        e = int(idx[order[p]])
+        want = w[e].double() @ x[int(order[p]) // 6].double()
+        got = first[p].double()
+        assert float((got - want).abs().max() / want.abs().max()) < 3e-3, int(p)
+    del w, x
+
+
 def test_grouped_gemm_addresses_operands_beyond_4gib(device):
     """Activation rows and an expert's weights that start past 4 GiB of their
     tensors (lane addresses are 64-bit; nothing is reduced mod 2^32).  Only the
