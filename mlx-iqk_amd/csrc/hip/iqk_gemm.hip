@@ -348,16 +348,18 @@ void grouped_gemm_lds_kernel(GemmArgs a) {
     const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
     const uint32_t a_lds = lds_offset(ast) + wv * (8 * kLdsRow);
     const uint32_t b_lds = lds_offset(bst) + wv * (kLdsWaveRows * kLdsRow);
-    // steps past the last re-read it into a stage nobody reads
+    // A load for a step past the last re-reads the last step's bytes (in
+    // bounds) into the stage of step s, which no later step reads: that stage
+    // held step s - 3 (activations) or s - 4 (weights), already consumed.
     const auto issue_a = [&](uint32_t s) {
-        s = min(s, ksteps - 1);
-        load_to_lds16(a_lds + (s % kLdsAStages) * kLdsAStage, asrc + s * kGemmBK);
+        const uint32_t k = min(s, ksteps - 1);
+        load_to_lds16(a_lds + (s % kLdsAStages) * kLdsAStage, asrc + k * kGemmBK);
     };
     const auto issue_b = [&](uint32_t s) {
-        s = min(s, ksteps - 1);
+        const uint32_t k = min(s, ksteps - 1);
 #pragma unroll
         for (int u = 0; u < kGemmU; ++u)
-            load_to_lds16(b_lds + (s % kLdsBStages) * kLdsBStage + 8 * kLdsRow * u, bsrc[u] + s * kGemmBK);
+            load_to_lds16(b_lds + (s % kLdsBStages) * kLdsBStage + 8 * kLdsRow * u, bsrc[u] + k * kGemmBK);
     };
     issue_b(0);
     issue_a(0);
