@@ -403,9 +403,10 @@ def test_grouped_gemm_addresses_operands_beyond_4gib(device):
     del x, w
 
 
-# K a multiple of 64 takes the direct-to-LDS kernel (one to many steps), other K the general one
-@pytest.mark.parametrize("K,N", [(4096, 2048), (2048, 4096), (2048, 256), (2048, 32), (4096, 272), (64, 256), (192, 40),
-                                 (2080, 96), (96, 288)])
+# K a multiple of 64 takes the direct-to-LDS kernel (one to many steps; at one, two and three
+# steps the loads past the last step start in the prologue), other K the general one
+@pytest.mark.parametrize("K,N", [(4096, 2048), (2048, 4096), (2048, 256), (2048, 32), (4096, 272), (64, 256), (128, 64),
+                                 (192, 40), (2080, 96), (96, 288)])
 def test_grouped_gemm_matches_a_float64_reference(device, K, N):
     print(f"grouped gemm K={K} N={N}", flush=True)
     rng = np.random.default_rng(K + N)
