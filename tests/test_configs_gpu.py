@@ -159,6 +159,12 @@ def test_iq2_ks_routed_decode_1_token(device):
     _decode_case(device, "iq2_ks", 1, seed=202)
 
 
+def test_iq2_ks_routed_decode_8_tokens(device):
+    """IQ2_KS, 256 experts, 8 tokens x top-6: the gate's three pairs of a token
+    a workgroup and the down's two-row-block form, as for IQ2_K."""
+    _decode_case(device, "iq2_ks", 8, seed=208)
+
+
 @pytest.mark.parametrize("which", ("gate", "down"))
 def test_decode_is_deterministic(device, which):
     """The same dispatch twice: identical fp16 bits (no atomics, fixed order),
