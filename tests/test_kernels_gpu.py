@@ -403,6 +403,32 @@ def test_grouped_gemm_addresses_operands_beyond_4gib(device):
     del x, w
 
 
+@pytest.mark.parametrize("K", (128, 96))
+def test_grouped_gemm_over_more_groups_than_one_scan_round(device, K):
+    """600 groups: the in-block work-list scan takes 256 a round (three rounds),
+    with empty, one-slot and multi-tile groups in each; every slot against a
+    float64 reference.  K = 128 takes the direct-to-LDS kernel, 96 the general
+    one."""
+    print(f"grouped gemm 600 groups K={K}", flush=True)
+    rng = np.random.default_rng(K + 600)
+    G, N = 600, 64
+    counts = rng.integers(0, 4, size=G)
+    counts[[3, 255, 256, 300, 511, 512, 599]] = [70, 65, 0, 64, 1, 0, 130]
+    P = int(counts.sum())
+    w = (rng.standard_normal((G, N, K)) * 0.05).astype(np.float16)
+    xrows = 512
+    x = rng.standard_normal((xrows, K)).astype(np.float16)
+    x_rows = rng.integers(0, xrows, size=P).astype(np.int32)
+    offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    got = kernels.grouped_gemm(torch.from_numpy(x).to(device), torch.from_numpy(w).to(device),
+                               torch.from_numpy(offs).to(device),
+                               torch.from_numpy(x_rows).to(device)).cpu().numpy().astype(np.float64)
+    g_of = np.repeat(np.arange(G), counts)
+    want = np.einsum("pk,pnk->pn", x[x_rows].astype(np.float64), w[g_of].astype(np.float64))
+    rel = np.max(np.abs(got - want)) / np.max(np.abs(want))
+    assert rel < 3e-3, rel
+
+
 # K a multiple of 64 takes the direct-to-LDS kernel (one to many steps; at one, two and three
 # steps the loads past the last step start in the prologue), other K the general one
 @pytest.mark.parametrize("K,N", [(4096, 2048), (2048, 4096), (2048, 256), (2048, 32), (4096, 272), (64, 256), (128, 64),

@@ -547,6 +547,28 @@ def test_fused_prefill_matches_the_producer_route(device, member, n):
 
 
 @pytest.mark.parametrize("member", fmt.MEMBERS)
+def test_prefill_over_more_experts_than_one_scan_round(device, member):
+    """600 experts: the GEMMs' in-block work-list scan takes 256 groups a
+    round, so three rounds, with empty, one-slot and multi-tile experts in
+    each (the largest, 130 slots, in the last round).  Both routes meet the
+    float64 gate and agree with each other."""
+    E, out, n = 600, 64, 2048
+    print(f"prefill over {E} experts {member}", flush=True)
+    module, ref = _module(member, n, wirepack.seed_for(member, n, "many"), device, out=out, experts=E)
+    rng = np.random.default_rng(149)
+    counts = rng.integers(0, 4, size=E)
+    counts[[3, 255, 256, 300, 511, 512, 599]] = [70, 65, 0, 64, 1, 0, 130]
+    idx = np.repeat(np.arange(E), counts).astype(np.int32).reshape(-1, 1)
+    x = rng.standard_normal((idx.shape[0], 1, 1, n)).astype(np.float16)
+    xt, it = torch.from_numpy(x).to(device), torch.from_numpy(idx).to(device)
+    fused, producer = _both_routes(module, xt, it, sorted_indices=True)
+    want = oracle.prefill_reference(ref, x, idx)
+    assert _rel(fused, want) < 3e-3 and _rel(producer, want) < 3e-3
+    diff = (fused.float() - producer.float()).abs().max().item()
+    assert diff <= 2e-3 * producer.float().abs().max().item()
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
 @pytest.mark.parametrize("out", (48, 272))
 def test_fused_prefill_serves_partial_row_blocks_and_several_rows_per_pair(device, member, out):
     """out_features not a multiple of the 256-row block; x [T, M, in] with M = 3
