@@ -124,7 +124,7 @@ void grouped_gemm_kernel(GemmArgs a) {
         const uint32_t ap = m0 + uint32_t(row);
         const uint32_t xrow = ap < gend ? a.xr[ap] : a.n_x_rows;
         const bool alive = xrow < a.n_x_rows;
-        asrc[i] = a.x + size_t(alive ? xrow : 0u) * a.K + 8 * achunk;
+        asrc[i] = a.x + size_t(alive ? xrow : 0u) * a.K;
         if (achunk == 0) {  // one thread a slot: the epilogue's destination, read once
             uint32_t dst = kNoStore;
             if (ap < gend) {
@@ -142,9 +142,12 @@ void grouped_gemm_kernel(GemmArgs a) {
         s = min(s, ksteps - 1);
 #pragma unroll
         for (int i = 0; i < kGemmAPer; ++i) {
-            uint32_t k = s * kGemmBK;
-            const bool live = k + 8 * achunk < a.K;
-            k = min(k, a.K - 8 * achunk - 8);
+            // the element offset in the row, clamped to its last 8 elements
+            // (K >= 32, so K - 8 does not wrap): a chunk past K reads inside
+            // its own row and is zeroed
+            uint32_t k = s * kGemmBK + 8 * achunk;
+            const bool live = k < a.K;
+            k = min(k, a.K - 8);
             const uint4_t t = load_u4(asrc[i] + k);
             v[i] = live ? t : uint4_t{0u, 0u, 0u, 0u};
         }
@@ -380,10 +383,11 @@ void grouped_gemm_lds_kernel(GemmArgs a) {
     const auto run_steps = [&](auto slot_blocks) {
         constexpr int MB = decltype(slot_blocks)::value;
         for (uint32_t s = 0; s < ksteps; ++s) {  // the step count is uniform
-            // this wavefront's A(s) and B(s) have landed; after the barrier
-            // every wavefront's A(s) has, and every wavefront is done with
-            // step s - 1, whose stages the loads below refill
-            asm volatile("s_waitcnt vmcnt(9)\n\ts_barrier" ::: "memory");
+            // this wavefront's A(s) and B(s) have landed and its LDS reads of
+            // step s - 1 have returned; after the barrier every wavefront's
+            // A(s) has landed, and every wavefront is done with step s - 1,
+            // whose stages the loads below refill
+            asm volatile("s_waitcnt vmcnt(9) lgkmcnt(0)\n\ts_barrier" ::: "memory");
             issue_a(s + 2);
             issue_b(s + 3);
             const uint8_t *ab = ast + (s % kLdsAStages) * kLdsAStage + ln * kLdsRow;

@@ -120,7 +120,11 @@ extern "C" int iqk_route(const uint32_t *ids, int64_t n_pairs, int64_t num_exper
     using namespace iqk;
     if (num_experts <= 0 || num_experts > kRouteMaxExperts) return IQK_ERR_ARGUMENT;
     if (n_pairs < 0 || rows_per_pair <= 0 || pairs_per_x_row <= 0 || n_x_rows < 0) return IQK_ERR_ARGUMENT;
-    if (n_pairs * rows_per_pair >= (int64_t(1) << 31) || n_x_rows >= (int64_t(1) << 31)) return IQK_ERR_ARGUMENT;
+    // each factor bounded first, so the products below cannot overflow
+    constexpr int64_t kLim = int64_t(1) << 31;
+    if (n_pairs >= kLim || rows_per_pair >= kLim || pairs_per_x_row >= kLim || n_x_rows >= kLim)
+        return IQK_ERR_ARGUMENT;
+    if (n_pairs * rows_per_pair >= kLim) return IQK_ERR_ARGUMENT;
     if (!group_offsets || (n_pairs && (!ids || !x_rows || !y_rows))) return IQK_ERR_ARGUMENT;
     // every activation row a valid pair names lies in x
     if (n_pairs && ((n_pairs - 1) / pairs_per_x_row + 1) * rows_per_pair > n_x_rows) return IQK_ERR_ARGUMENT;

@@ -121,7 +121,9 @@ class CheckedStreams:
     one GPU, contiguity): the device and the pointer array the launchers pass.
     Every launcher takes one in place of the stream list and skips its checks;
     it stays valid while the tensors do (``IqkSwitchLinear`` drops its copy
-    whenever a stream is reassigned or the module is moved)."""
+    whenever a stream is reassigned or the module is moved, and makes a new
+    one whenever a stream's address, shape, strides or dtype differ from the
+    ones it was made from)."""
 
     __slots__ = ("key", "device", "ptrs", "count")
 

@@ -99,9 +99,12 @@ class IqkSwitchLinear(torch.nn.Module):
         for name, shape in component_shapes(member, num_experts, out_features, in_features).items():
             self.register_buffer(name, torch.zeros(shape, dtype=dtypes[name], device=device))
         # the streams checked once for the launchers (kernels.CheckedStreams),
-        # dropped whenever a stream is reassigned or the module moves
+        # dropped whenever a stream is reassigned or the module moves, and
+        # re-checked whenever a stream's storage, shape or dtype differs from
+        # the record's (register_buffer and ``.data =`` bypass __setattr__)
         object.__setattr__(self, "_stream_set", frozenset(self.stream_names()))
         object.__setattr__(self, "_checked_streams", None)
+        object.__setattr__(self, "_checked_sig", None)
 
     def __setattr__(self, name, value):
         if name in self.__dict__.get("_stream_set", ()):
@@ -113,10 +116,14 @@ class IqkSwitchLinear(torch.nn.Module):
         return super()._apply(fn, *args, **kwargs)
 
     def _checked(self) -> kernels.CheckedStreams:
-        """The streams as the launchers take them, checked on first use."""
-        if self._checked_streams is None:
+        """The streams as the launchers take them, checked on first use and
+        again whenever a stream tensor's address, shape or dtype has changed."""
+        streams = self._streams()
+        sig = tuple((t.data_ptr(), t.shape, t.stride(), t.dtype, t.device) for t in streams)
+        if self._checked_streams is None or sig != self._checked_sig:
             object.__setattr__(self, "_checked_streams", kernels.CheckedStreams(
-                self.member, self._streams(), self.num_experts, self.out_features, self.in_features))
+                self.member, streams, self.num_experts, self.out_features, self.in_features))
+            object.__setattr__(self, "_checked_sig", sig)
         return self._checked_streams
 
     # -- the relayout streams (module buffers) ---------------------------------

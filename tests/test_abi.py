@@ -158,6 +158,10 @@ def test_route_refuses_bad_arguments(lib):
     assert f(None, 8, 8, 1, 1, 8, p, p, p, None) == _native.ERR_ARGUMENT
     assert f(p, 8, 8, 1, 1, 8, None, p, p, None) == _native.ERR_ARGUMENT
     assert f(p, 1 << 30, 8, 2, 1, 1 << 31, p, p, p, None) == _native.ERR_ARGUMENT  # 2^31 slots
+    # factors whose int64 product would overflow (2^33 x 2^31) and wrap below 2^31
+    assert f(p, 1 << 33, 8, 1 << 31, 1, 8, p, p, p, None) == _native.ERR_ARGUMENT
+    assert f(p, 1 << 40, 8, 1 << 24, 1, 8, p, p, p, None) == _native.ERR_ARGUMENT  # 2^64: wraps to 0
+    assert f(p, 8, 8, 1, 1 << 32, 8, p, p, p, None) == _native.ERR_ARGUMENT  # pairs per x row past 32 bits
 
 
 def test_pack_refuses_bad_arguments(lib):

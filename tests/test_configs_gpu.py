@@ -94,13 +94,39 @@ def _check_decode(got, want, label):
     return rel, l2, exact
 
 
-def _decode_case(device, member, tokens, seed):
+def _quantized_stack(member, out, n, seed, device, distinct=4):
+    """A 256-expert module whose rows are N(0, 0.02) rows quantized by the
+    package codec under a U(0.1, 1) imatrix (the workloads' stacks).
+    Quantizing 256 experts is minutes of host search, so ``distinct`` experts
+    are quantized and expert e holds tile e % distinct with its rows rotated
+    by e // distinct (whole four-row groups), as the benchmark's stacks are
+    built; every expert still owns its bytes at its own address."""
+    key = ("quantized", member, out, n, seed)
+    if key not in _STACKS:
+        print(f"  quantizing {member} {distinct}x{out}x{n} (seed {seed}) into a {E}-expert stack", flush=True)
+        tiles = [synth.quantized_rows(member, out, n, seed + t, imatrix_seed=seed + 1000) for t in range(distinct)]
+        group = 4 if member == "iq1_s_r4" else 1
+        wire = np.empty((E * out, tiles[0].shape[1]), dtype=np.uint8)
+        for e in range(E):
+            shift = group * ((e // distinct) % (out // group))
+            wire[e * out:(e + 1) * out] = np.roll(tiles[e % distinct], shift, axis=0)
+        module = IqkSwitchLinear(member, E, out, n, device=device)
+        module.load_wire(torch.from_numpy(wire).to(device))
+        torch.cuda.synchronize()
+        _STACKS[key] = (module, wire)
+    return _STACKS[key]
+
+
+def _decode_case(device, member, tokens, seed, quantized=False):
     """Gate and down projections of one routed decode step: every pair, 64 sampled rows each."""
     rng = np.random.default_rng(seed)
     idx = np.stack([rng.choice(E, TOP_K, replace=False) for _ in range(tokens)]).astype(np.int32)
     it = torch.from_numpy(idx).to(device)
     for name, (out, n), x_shape in (("gate", GU, (tokens, 1, 1, GU[1])), ("down", DN, (tokens, TOP_K, 1, DN[1]))):
-        module, wire = _stack(member, out, n, wirepack.seed_for("config", member, name), device)
+        if quantized:
+            module, wire = _quantized_stack(member, out, n, wirepack.seed_for("quantized", member, name), device)
+        else:
+            module, wire = _stack(member, out, n, wirepack.seed_for("config", member, name), device)
         x = rng.standard_normal(x_shape).astype(np.float16)
         print(f"  {member} {name} {tokens} token(s) x top-{TOP_K}", flush=True)
         y = module(torch.from_numpy(x).to(device), it)
@@ -163,6 +189,39 @@ def test_iq2_ks_routed_decode_8_tokens(device):
     """IQ2_KS, 256 experts, 8 tokens x top-6: the gate's three pairs of a token
     a workgroup and the down's two-row-block form, as for IQ2_K."""
     _decode_case(device, "iq2_ks", 8, seed=208)
+
+
+@pytest.mark.parametrize("member, tokens", (("iq2_ks", 1), ("iq2_k", 8), ("iq1_s_r4", 1)))
+def test_routed_decode_on_codec_quantized_stacks(device, member, tokens):
+    """The routed decode workloads on stacks quantized by the package codec
+    from N(0, 0.02) rows (IQ2_KS 1 token, IQ2_K 8 tokens, IQ1_S_R4 1 token;
+    top-6 over 256 experts, both geometries), against float64 contractions of
+    the oracle's dequantization of the same wire."""
+    _decode_case(device, member, tokens, seed=707 + tokens, quantized=True)
+
+
+@pytest.mark.parametrize("member", ("iq2_ks", "iq1_s_r4"))
+def test_row_range_producer_at_the_gate_geometry(device, member):
+    """The row-range producer at [2048 x 4096] over 256 experts: a token's six
+    experts compacted into slots in expert order, ranges from a half expert
+    down to one four-row group, each slot's rows the oracle's bit for bit
+    (reference range form: src/mlx_iqk/nn.py:171-201)."""
+    from mlx_iqk_amd import kernels
+    out, n = GU
+    module, wire = _stack(member, out, n, wirepack.seed_for("config", member, "gate"), device)
+    rng = np.random.default_rng(606)
+    experts = np.sort(rng.choice(E, TOP_K, replace=False))
+    slot_of = np.full(E, -1, dtype=np.int32)
+    slot_of[experts] = np.arange(TOP_K, dtype=np.int32)
+    sot = torch.from_numpy(slot_of).to(device)
+    for start, rows in ((0, 1024), (1024, 1024), (512, 64), (2044, 4)):
+        print(f"  {member} range [{start}, +{rows}) of experts {experts.tolist()}", flush=True)
+        got = kernels.dequant(member, module._checked(), E, out, n, slot_of_expert=sot, n_slots=TOP_K,
+                              row_start=start, rows=rows)
+        got = got.view(torch.int16).cpu().numpy()
+        for s, e in enumerate(experts):
+            want = oracle.dequantize(member, wire[e * out + start:e * out + start + rows], n)
+            assert np.array_equal(got[s], want.astype(np.float16).view(np.int16)), (member, start, rows, int(e))
 
 
 @pytest.mark.parametrize("which", ("gate", "down"))

@@ -430,9 +430,10 @@ def test_grouped_gemm_over_more_groups_than_one_scan_round(device, K):
 
 
 # K a multiple of 64 takes the direct-to-LDS kernel (one to many steps; at one, two and three
-# steps the loads past the last step start in the prologue), other K the general one
+# steps the loads past the last step start in the prologue), other K the general one (K = 32:
+# one half step, the upper chunks of every row clamped inside that row)
 @pytest.mark.parametrize("K,N", [(4096, 2048), (2048, 4096), (2048, 256), (2048, 32), (4096, 272), (64, 256), (128, 64),
-                                 (192, 40), (2080, 96), (96, 288)])
+                                 (192, 40), (2080, 96), (96, 288), (32, 64), (32, 264)])
 def test_grouped_gemm_matches_a_float64_reference(device, K, N):
     print(f"grouped gemm K={K} N={N}", flush=True)
     rng = np.random.default_rng(K + N)
@@ -442,6 +443,7 @@ def test_grouped_gemm_matches_a_float64_reference(device, K, N):
     xrows = 300
     x = rng.standard_normal((xrows, K)).astype(np.float16)
     x_rows = rng.integers(0, xrows, size=P).astype(np.int32)
+    x_rows[[0, 1, P - 1]] = xrows - 1  # the last row of x, where a load past its row would leave x
     y_rows = rng.permutation(P).astype(np.int32)
     offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
     got = kernels.grouped_gemm(torch.from_numpy(x).to(device), torch.from_numpy(w).to(device),

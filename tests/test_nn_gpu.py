@@ -475,12 +475,40 @@ def test_union_gemv_at_the_routed_geometry(device, member):
 @pytest.mark.parametrize("member", fmt.MEMBERS)
 @pytest.mark.parametrize("n", (2048, 4096))
 def test_dequantized_range_matches_the_full_slice(device, member, n):
-    module, _ = _module(member, n, wirepack.seed_for(member, n, "range"), device)
+    """Every range is the same slice of the full reconstruction and of the
+    oracle's dequantization (fp16 bits: the CPU dequantizer's float32 values
+    rounded once)."""
+    module, ref = _module(member, n, wirepack.seed_for(member, n, "range"), device)
     full = _bits(module.dequantized())
+    want = ref.astype(np.float16).view(np.int16)
+    assert np.array_equal(full, want)
     for start, rows in ((0, 8), (8, 8), (16, 16), (0, 32), (24, 8), (3, 1), (5, 2), (0, OUT), (128, 128)):
         got = _bits(module.dequantized_range(start, rows))
         assert got.shape == (EXPERTS, rows, n), (start, rows)
         assert np.array_equal(got, full[:, start:start + rows]), (start, rows)
+        assert np.array_equal(got, want[:, start:start + rows]), (start, rows)
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+def test_dequantized_range_into_compacted_slots_matches_the_oracle(device, member):
+    """Ranges of the experts a routing names, compacted into slots in expert
+    order (the producer route's form): each slot holds the oracle's rows of its
+    expert, bit for bit; slots no expert maps to stay as they were."""
+    n = 2048
+    module, ref = _module(member, n, wirepack.seed_for(member, n, "range-slots"), device)
+    experts = [6, 1, 4]  # slot s <- experts[s]
+    slot_of = np.full(EXPERTS, -1, dtype=np.int32)
+    slot_of[experts] = np.arange(len(experts))
+    sot = torch.from_numpy(slot_of).to(device)
+    want = ref.astype(np.float16).view(np.int16)
+    for start, rows in ((0, OUT), (64, 64), (4, 4), (252, 4), (96, 32)):
+        out = torch.full((len(experts) + 1, rows, n), float("nan"), dtype=torch.float16, device=device)
+        got = kernels.dequant(member, module._checked(), EXPERTS, OUT, n, slot_of_expert=sot,
+                              n_slots=len(experts) + 1, row_start=start, rows=rows, out=out)
+        got = _bits(got)
+        for s, e in enumerate(experts):
+            assert np.array_equal(got[s], want[e, start:start + rows]), (start, rows, e)
+        assert np.isnan(out[len(experts)].float().cpu().numpy()).all(), (start, rows)
 
 
 @pytest.mark.parametrize("member", fmt.MEMBERS)
@@ -513,6 +541,35 @@ def test_sorted_matmul_range_concat_matches_the_sorted_call(device, member, n):
     narrow = torch.cat([module.sorted_matmul_range(x, idx, 64 + 8 * i, 8) for i in range(2)]
                        + [module.sorted_matmul_range(x, idx, 80, 1)], dim=-1)
     assert np.array_equal(_bits(narrow), _bits(full[..., 64:81]))
+
+
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+@pytest.mark.parametrize("fused", (False, True))
+def test_sorted_matmul_range_matches_a_float64_reference(device, member, fused):
+    """Each route's ranged prefill (the producer's row range + grouped GEMM,
+    and the fused contraction over the range) against float64 contractions
+    of the oracle's rows of that range: the reference's prefill gate, < 3e-3
+    of the output range (tests/test_nn.py:337-378)."""
+    n = 2048
+    module, ref = _module(member, n, wirepack.seed_for(member, n, "range-f64"), device)
+    module.fused_prefill = fused
+    rng = np.random.default_rng(71)
+    tokens, top_k = 20, 4
+    xh = rng.standard_normal((tokens, 1, 1, n)).astype(np.float16)
+    idx = rng.integers(0, EXPERTS, size=(tokens, top_k)).astype(np.int32)
+    x = torch.from_numpy(xh).to(device)
+    it = torch.from_numpy(idx).to(device)
+    try:
+        for start, rows in ((0, 128), (128, 64), (200, 8), (31, 1), (0, OUT)):
+            got = module.sorted_matmul_range(x, it, start, rows)
+            assert tuple(got.shape) == (tokens, top_k, 1, rows), (start, rows)
+            got = got.float().cpu().numpy().astype(np.float64).reshape(tokens, top_k, rows)
+            want = np.stack([[ref[e, start:start + rows].astype(np.float64) @ xh[t, 0, 0].astype(np.float64)
+                              for e in idx[t]] for t in range(tokens)])
+            rel = np.max(np.abs(got - want)) / np.max(np.abs(want))
+            assert rel < 3e-3, (start, rows, rel)
+    finally:
+        module.fused_prefill = True
 
 
 # -- fused prefill (the producer's weights formed inside the GEMM) ----------
