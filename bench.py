@@ -80,10 +80,11 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--block", type=int, default=200, help="dispatches per captured graph in a cell")
     ap.add_argument("--blocks", type=int, default=4, help="graph replays per arm and round; the best one counts")
     ap.add_argument("--distinct", type=int, default=2, help="distinct quantized experts per projection")
-    ap.add_argument("--cells", default="iq2_ks,iq2_k,iq1_s_r4,dequant,prefill,pack,verify,quantize",
+    ap.add_argument("--cells", default="iq2_ks,module,iq2_k,iq1_s_r4,dequant,prefill,pack,verify,quantize",
                     help="cells after the headline ('headline' alone: the IQ2_KS cell and the headline only)")
-    ap.add_argument("--cpu-seconds", type=float, default=20.0,
-                    help="CPU baseline sample budget (half on one thread, half on every core)")
+    ap.add_argument("--cpu-seconds", type=float, default=30.0,
+                    help="CPU baseline sample budget over its four workloads (each half on one thread, half on "
+                         "every core)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--json-out", default=None)
     ap.add_argument("--probe", type=int, default=0, metavar="K",
@@ -100,11 +101,13 @@ def parse() -> argparse.Namespace:
 
 
 class Arm:
-    """A captured graph of `count` dispatches; time() replays it once."""
+    """A captured graph of `count` dispatches; time() replays it once.  The
+    eager warm-up before capture runs `warm` (default: the first four
+    launches)."""
 
-    def __init__(self, torch, launches, label):
+    def __init__(self, torch, launches, label, warm=None):
         self.torch, self.label, self.count = torch, label, len(launches)
-        for fn in launches[: min(4, len(launches))]:
+        for fn in (launches[: min(4, len(launches))] if warm is None else warm):
             fn()  # eager warm-up outside capture
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
@@ -168,12 +171,17 @@ class StreamWindows:
         self.buf = torch.zeros(STREAM_BUFFER_BYTES, dtype=torch.uint8, device=device)
         self.out = torch.empty(STREAM_BUFFER_BYTES // 4096, dtype=torch.int32, device=device)
 
-    def launcher(self, nbytes: int, i: int):
+    # the forms of the stream: (KiB in flight a wavefront, wavefront cap: 0 =
+    # one wavefront a chunk; 2048 = eight a CU, striding over the span)
+    FORMS = {"stream": (4, 0), "stream_w8": (8, 0), "stream_w16": (16, 0), "stream_gs": (16, 2048)}
+
+    def launcher(self, nbytes: int, i: int, form: str = "stream"):
         from mlx_iqk_amd import kernels
-        span = (nbytes + 4095) // 4096 * 4096
+        loads, max_waves = self.FORMS[form]
+        span = (nbytes + 16383) // 16384 * 16384
         slots = max(1, STREAM_BUFFER_BYTES // span)
         view = self.buf[(i % slots) * span:]
-        return lambda: kernels.stream_floor(view, nbytes, out=self.out)
+        return lambda: kernels.stream_floor(view, nbytes, out=self.out, loads=loads, max_waves=max_waves)
 
 
 def gate_cell(res: dict, bar: float) -> dict:
@@ -253,7 +261,8 @@ def decode_cell(torch, device, member: str, tokens: int, args, seed: int, want_s
         arms = {"decode": Arm(torch, [launch(i) for i in range(B)], "decode"),
                 "floor": Arm(torch, [launch(i, True) for i in range(B)], "floor")}
         if windows is not None:
-            arms["stream"] = Arm(torch, [windows.launcher(nbytes, i) for i in range(B)], "stream")
+            for form in windows.FORMS:
+                arms[form] = Arm(torch, [windows.launcher(nbytes, i, form) for i in range(B)], form)
         if member == "iq1_s_r4":
             arms["floor_grid"] = Arm(torch, [launch(i, "grid") for i in range(B)], "floor_grid")
         res = alternate(arms, args.rounds, args.blocks)
@@ -263,7 +272,11 @@ def decode_cell(torch, device, member: str, tokens: int, args, seed: int, want_s
             res[arm]["frac_of_8tbps"] = round(res[arm]["gb_per_s"] / HBM_PEAK_GBS, 4)
         res["x_floor"] = round(res["decode"]["median_us"] / res["floor"]["median_us"], 4)
         if "stream" in arms:
-            res["x_stream"] = round(res["decode"]["median_us"] / res["stream"]["median_us"], 4)
+            # against the fastest form of the byte stream at this size
+            best = min(StreamWindows.FORMS, key=lambda f: res[f]["median_us"])
+            res["stream_best"] = best
+            res["x_stream"] = round(res["decode"]["median_us"] / res[best]["median_us"], 4)
+            res["x_stream_4k"] = round(res["decode"]["median_us"] / res["stream"]["median_us"], 4)
         if "floor_grid" in arms:
             res["x_floor_grid"] = round(res["decode"]["median_us"] / res["floor_grid"]["median_us"], 4)
         res["ideal_us_at_8tbps"] = round(nbytes / HBM_PEAK_GBS / 1e3, 3)
@@ -273,7 +286,8 @@ def decode_cell(torch, device, member: str, tokens: int, args, seed: int, want_s
         cells[name] = res
         log(f"  {name:8s} decode {res['decode']['median_us']:8.2f} us ({res['decode']['gb_per_s']:7.1f} GB/s)"
             f"  floor {res['floor']['median_us']:8.2f} us  x{res['x_floor']:.3f}"
-            + (f"  stream {res['stream']['median_us']:.2f} us x{res['x_stream']:.3f}" if "stream" in res else "")
+            + (f"  stream " + "/".join(f"{res[f]['median_us']:.2f}" for f in StreamWindows.FORMS)
+               + f" us x{res['x_stream']:.3f}" if "stream" in res else "")
             + (f"  grid floor {res['floor_grid']['median_us']:.2f} us x{res['x_floor_grid']:.3f}"
                if "floor_grid" in res else ""))
         del arms
@@ -285,15 +299,18 @@ def decode_cell(torch, device, member: str, tokens: int, args, seed: int, want_s
 
 
 def headline(torch, step, steps: int, warmup: int):
-    """The timed region: K steps (gate/up + down) replayed as one graph."""
+    """The timed region: K steps (gate/up + down) replayed as one graph.  The
+    W warm-up steps run the routing variants of the region's last W steps,
+    never its first ones, so the region starts with experts that no recent
+    launch has read (out of the 256 MB MALL)."""
     gu_launch, dn_launch, nbytes = step
-    for i in range(warmup):
-        gu_launch(i)()
-        dn_launch(i)()
+    warm = []
+    for i in range(steps - warmup, steps):
+        warm += [gu_launch(i), dn_launch(i)]
     launches = []
     for i in range(steps):
         launches += [gu_launch(i), dn_launch(i)]
-    arm = Arm(torch, launches, "headline")
+    arm = Arm(torch, launches, "headline", warm=warm)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     us_per_launch = arm.time()
@@ -302,6 +319,60 @@ def headline(torch, step, steps: int, warmup: int):
     ms_per_step = us_per_launch * 2 / 1e3
     return {"ms_per_step": ms_per_step, "wall_s": wall, "gb_per_s": nbytes / (ms_per_step * 1e-3) / 1e9,
             "bytes_per_step": nbytes}
+
+
+def module_cell(torch, device, args, seed: int):
+    """The decode dispatches the switch module itself issues at 1 token (the
+    reference's SwitchGLU calls gate, up and down projections separately):
+    IqkSwitchLinear gate [2048 x 4096] alone (6 pairs: 384 workgroups of 32
+    rows, against the 768 of the bench's combined gate+up dispatch) and down
+    [4096 x 2048] (6 pairs, 768 workgroups), each as a graph of 200 module
+    calls on disjoint routings, timed as the decode cells are; plus the host
+    time of an eager module call."""
+    from mlx_iqk_amd import synth
+    from mlx_iqk_amd.format import ik_row_bytes
+    from mlx_iqk_amd.nn import IqkSwitchLinear
+
+    member, B = "iq2_ks", args.block
+    rng = np.random.default_rng(seed)
+    sels = disjoint_selections(rng, 42, 1)
+    res = {"member": member, "tokens": 1, "top_k": TOP_K}
+    arms = {}
+    # every tensor a captured graph reads stays referenced here until the
+    # graphs are gone: the modules' streams, the activations and the ids
+    keep = []
+    for name, (out, n) in (("gate", GU), ("down", DN)):
+        mod = IqkSwitchLinear(member, EXPERTS, out, n, device=device)
+        for k, t in zip(mod.stream_names(), synth.expert_stack(member, EXPERTS, out, n, seed, device,
+                                                                 args.distinct, f"module-{name}")):
+            setattr(mod, k, t)
+        ids = [torch.from_numpy(s_.astype(np.int32)).to(device) for s_ in sels]
+        shape = (1, 1, 1, n) if name == "gate" else (1, TOP_K, 1, n)
+        xs = [torch.randn(shape, device=device).to(torch.float16) for _ in sels]
+        keep.append((mod, ids, xs))
+        call = lambda i, mod=mod, ids=ids, xs=xs: (lambda: mod(xs[i % len(xs)], ids[i % len(ids)]))  # noqa: E731
+        arms[name] = Arm(torch, [call(i) for i in range(B)], name)
+        # host time of an eager call (the launch path: shape checks, the cached stream record, one launch)
+        for i in range(20):
+            call(i)()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(B):
+            call(i)()
+        host = (time.perf_counter() - t0) * 1e6 / B
+        torch.cuda.synchronize()
+        res[name] = {"bytes_per_call": TOP_K * out * ik_row_bytes(member, n), "host_us_per_eager_call": round(host, 2),
+                     "workgroups": TOP_K * out // 32}
+    r = alternate(arms, args.rounds, args.blocks)
+    del arms  # the graphs first, then the tensors they read
+    torch.cuda.synchronize()
+    keep.clear()
+    for name in ("gate", "down"):
+        res[name].update(r[name])
+        res[name]["gb_per_s"] = round(res[name]["bytes_per_call"] / (r[name]["median_us"] * 1e-6) / 1e9, 1)
+    log(f"[module {member} x1] gate alone {res['gate']['median_us']:.2f} us ({res['gate']['gb_per_s']} GB/s), "
+        f"down {res['down']['median_us']:.2f} us; eager host {res['gate']['host_us_per_eager_call']:.1f} us a call")
+    return res
 
 
 # ---------------------------------------------------------------- producer cell ---
@@ -651,68 +722,183 @@ def _cpu_model() -> str:
     return cpu
 
 
-def cpu_baseline(seconds: float, distinct: int, seed: int) -> dict:
-    """The reference's CPU dequantizer + float32 matmul on the headline step's
-    selected experts (6 x gate, up, down), on a bounded sample: once on one
-    thread, once on every host core (one matrix per worker; the compiled
-    dequantizer releases the GIL, numpy's BLAS is held to one thread per
-    worker).  The all-core run is the reported value."""
+class _CpuPath:
+    """The reference's CPU path for one workload: its CPU dequantizer on ik
+    wire, then numpy float32 matmuls, on the experts a routing selects.
+    ``job`` gives one job (one expert matrix); a job returns its seconds of
+    dequantization and of matmul."""
+
+    _local = None
+
+    def __init__(self, deq, member: str, tiles: dict):
+        import threading
+        if _CpuPath._local is None:
+            _CpuPath._local = threading.local()  # a worker's float32 weight buffers, reused across its jobs
+        self.deq, self.member, self.tiles = deq, member, tiles
+
+    @staticmethod
+    def buffers() -> dict:
+        """This worker's buffers for both geometries, allocated and resident."""
+        bufs = getattr(_CpuPath._local, "bufs", None)
+        if bufs is None:
+            bufs = _CpuPath._local.bufs = {}
+            for shape in (GU, DN):
+                bufs[shape] = np.ones(shape, dtype=np.float32)
+        return bufs
+
+    def job(self, geometry: str, e: int, x: np.ndarray):
+        def run():
+            wire = self.tiles[geometry][e % len(self.tiles[geometry])]
+            buf = self.buffers()[(wire.shape[0], x.shape[-1])]
+            t0 = time.perf_counter()
+            w = self.deq(self.member, wire, x.shape[-1], out=buf)
+            t1 = time.perf_counter()
+            _ = w @ x.T if x.ndim == 2 else w @ x
+            return t1 - t0, time.perf_counter() - t1
+        return run
+
+
+def _cpu_run(jobs_fn, threads: int, budget: float) -> dict:
+    """Whole steps of jobs on `threads` workers (numpy held to one thread a
+    worker; the compiled dequantizer releases the GIL) until `budget` seconds
+    have passed.  Untimed first: every worker allocates its buffers (all
+    workers at once, by a barrier) and one step runs."""
+    import threading
     from concurrent.futures import ThreadPoolExecutor
 
     from threadpoolctl import threadpool_limits
 
+    with threadpool_limits(limits=1), ThreadPoolExecutor(max_workers=threads) as pool:
+        barrier = threading.Barrier(threads)
+        list(pool.map(lambda _: (_CpuPath.buffers(), barrier.wait()), range(threads)))
+        list(pool.map(lambda f: f(), jobs_fn()))
+        done, dq, mm, t0 = 0, 0.0, 0.0, time.perf_counter()
+        while True:
+            for a, b in pool.map(lambda f: f(), jobs_fn()):
+                dq, mm = dq + a, mm + b
+            done += 1
+            if time.perf_counter() - t0 >= budget:
+                break
+    return {"steps": done, "seconds": time.perf_counter() - t0, "dequant_s": dq, "matmul_s": mm}
+
+
+def cpu_baseline(seconds: float, distinct: int, seed: int) -> dict:
+    """The reference's CPU path -- its CPU dequantizer (compiled from its own
+    sources, else the oracle's restatement) + numpy float32 matmul -- beside
+    each GPU workload, each on a bounded sample, once on one thread and once
+    on every host core:
+
+    * IQ2_KS 1 token (the headline step: 6 x gate, up, down GEMVs) -- the
+      reported ``value``, in the headline's unit;
+    * IQ2_K 8 tokens (48 pairs: each distinct expert dequantized once and
+      contracted with the tokens routed to it) and IQ1_S_R4 1 token, in the
+      same bytes-per-step convention as their GPU cells;
+    * the 2048-token Zipf(1.1) prefill (IQ2_KS gate/up, IQ2_K down): a
+      sample of the routed experts (each dequantized, then its slots
+      contracted), from which the time of the whole prefill's three
+      projections is extrapolated (dequantization per expert, matmul by
+      flops).
+    """
     from mlx_iqk_amd import format as fmt
     from mlx_iqk_amd import synth
     from oracle import oracle
 
     kind = "reference" if oracle.ref_available() else "port"
     deq = oracle.ref_dequantize if kind == "reference" else oracle.dequantize
-    member = "iq2_ks"
-    tiles = {}
-    for name, (out, n) in (("gate_up", GU), ("down", DN)):
-        tiles[name] = [synth.quantized_rows(member, out, n, synth.seed_for(seed, name, member, out, n, t),
-                                            imatrix_seed=synth.seed_for(seed, name, "imatrix", n))
-                       for t in range(distinct)]
-    rng = np.random.default_rng(seed)
-    x_gu = rng.standard_normal(GU[1]).astype(np.float16).astype(np.float32)
-    x_dn = rng.standard_normal((TOP_K, DN[1])).astype(np.float16).astype(np.float32)
-    step_bytes = 2 * TOP_K * GU[0] * fmt.ik_row_bytes(member, GU[1]) + TOP_K * DN[0] * fmt.ik_row_bytes(member, DN[1])
-
-    def matrix(job):
-        wire, n, x = job
-        return deq(member, wire, n) @ x
-
-    def step_jobs():
-        sel = rng.choice(EXPERTS, TOP_K, replace=False)
-        jobs = []
-        for k, e in enumerate(sel):
-            for p in range(2):  # gate, up
-                jobs.append((tiles["gate_up"][(e + p) % distinct], GU[1], x_gu))
-            jobs.append((tiles["down"][e % distinct], DN[1], x_dn[k]))
-        return jobs
-
-    def run(threads: int, budget: float) -> dict:
-        done, t0 = 0, time.perf_counter()
-        with threadpool_limits(limits=1), ThreadPoolExecutor(max_workers=threads) as pool:
-            while True:
-                list(pool.map(matrix, step_jobs()))
-                done += 1
-                if time.perf_counter() - t0 >= budget:
-                    break
-        elapsed = time.perf_counter() - t0
-        return {"value": round(done * step_bytes / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads,
-                "steps": done, "seconds": round(elapsed, 2), "ms_per_step": round(elapsed / done * 1e3, 2)}
-
     cores = len(os.sched_getaffinity(0))
-    matrix(step_jobs()[0])  # untimed: loads the dequantizer library before any worker starts
-    one = run(1, seconds / 2)
-    every = run(cores, seconds / 2)
-    return {"value": every["value"], "unit": "GB/s", "cores": cores, "kind": kind,
-            "sample": f"{every['steps']} headline steps ({every['steps'] * 18} matrices: the reference CPU "
-                      f"dequantizer on ik wire + numpy float32 GEMV, one matrix per worker on {cores} threads) "
-                      f"in {every['seconds']}s",
-            "ms_per_step": every["ms_per_step"], "single_thread": one, "cpu_model": _cpu_model(),
-            "host_cpus": cores}
+    rng = np.random.default_rng(seed)
+    tile_cache = {}
+
+    def tiles(member):
+        if member not in tile_cache:
+            tile_cache[member] = {
+                name: [synth.quantized_rows(member, out, n, synth.seed_for(seed, name, member, out, n, t),
+                                            imatrix_seed=synth.seed_for(seed, name, "imatrix", n))
+                       for t in range(distinct)] for name, (out, n) in (("gate_up", GU), ("down", DN))}
+        return tile_cache[member]
+
+    def decode_jobs(member: str, tokens: int):
+        """One routed decode step: gate and up (one activation row a token),
+        down (one row a pair); per distinct expert one dequantization."""
+        path = _CpuPath(deq, member, tiles(member))
+        xg = rng.standard_normal((tokens, GU[1])).astype(np.float16).astype(np.float32)
+        xd = rng.standard_normal((tokens * TOP_K, DN[1])).astype(np.float16).astype(np.float32)
+
+        def jobs():
+            sel = np.stack([rng.choice(EXPERTS, TOP_K, replace=False) for _ in range(tokens)])
+            out = []
+            for e in np.unique(sel):
+                toks = np.nonzero((sel == e).any(axis=1))[0]
+                pairs = np.flatnonzero(sel.reshape(-1) == e)
+                xt = xg[toks] if tokens > 1 else xg[0]
+                for p in range(2):  # gate, up
+                    out.append(path.job("gate_up", int(e) + p, xt))
+                out.append(path.job("down", int(e), xd[pairs] if tokens > 1 else xd[pairs[0]]))
+            return out
+        nbytes = tokens * TOP_K * (2 * GU[0] * fmt.ik_row_bytes(member, GU[1]) + DN[0] * fmt.ik_row_bytes(member, DN[1]))
+        return jobs, nbytes
+
+    def decode_entry(member, tokens, budget):
+        jobs, nbytes = decode_jobs(member, tokens)
+        jobs()[0]()  # untimed: loads the dequantizer library before any worker starts
+        one, every = _cpu_run(jobs, 1, budget / 2), _cpu_run(jobs, cores, budget / 2)
+        rate = lambda r: round(r["steps"] * nbytes / r["seconds"] / 1e9, 3)  # noqa: E731
+        return {"value": rate(every), "unit": "GB/s", "cores": cores, "single_thread": rate(one),
+                "ms_per_step": round(every["seconds"] / every["steps"] * 1e3, 2),
+                "sample": f"{every['steps']} + {one['steps']} steps of {tokens} token(s) x top-{TOP_K} "
+                          f"({member}; {cores} threads, then 1)"}
+
+    def prefill_entry(budget):
+        """The Zipf prefill's three projections, extrapolated from a sample of
+        routed experts (gate/up IQ2_KS, down IQ2_K), one expert a job."""
+        idx = synth.zipf_routing(2048, EXPERTS, TOP_K, 1.1, 23)
+        counts = np.bincount(idx.reshape(-1), minlength=EXPERTS)
+        routed = np.flatnonzero(counts)
+        x = {"gate_up": rng.standard_normal((int(counts.max()), GU[1])).astype(np.float16).astype(np.float32),
+             "down": rng.standard_normal((int(counts.max()), DN[1])).astype(np.float16).astype(np.float32)}
+        paths = {"iq2_ks": _CpuPath(deq, "iq2_ks", tiles("iq2_ks")), "iq2_k": _CpuPath(deq, "iq2_k", tiles("iq2_k"))}
+        projections = (("gate_up", "iq2_ks", GU), ("gate_up", "iq2_ks", GU), ("down", "iq2_k", DN))
+        total_flop = sum(2 * int(counts.sum()) * out * n for _, _, (out, n) in projections)
+        total_experts = len(projections) * routed.size
+        order = rng.permutation(routed)
+        state = {"k": 0}
+
+        def take(count):  # the next `count` (expert, projection) jobs of the shuffled order
+            out = []
+            for _ in range(count):
+                i = state["k"]
+                state["k"] += 1
+                e = int(order[i % order.size])
+                geo, member, _ = projections[i % 3]
+                out.append(paths[member].job(geo, e, x[geo][:int(counts[e])]))
+            return out
+
+        def entry(threads, share):
+            state["k"] = 0
+            r = _cpu_run(lambda: take(threads), threads, share)
+            n = state["k"]
+            picked = [(int(order[i % order.size]), projections[i % 3][2]) for i in range(n)]
+            flop = sum(2 * int(counts[e]) * out * k for e, (out, k) in picked)
+            # per-expert dequantization and flop-proportional matmul, scaled to the whole prefill
+            work = r["dequant_s"] * total_experts / n + r["matmul_s"] * total_flop / flop
+            return work * r["seconds"] / (r["dequant_s"] + r["matmul_s"]), n, r
+
+        take(1)[0]()
+        t1, n1, _ = entry(1, budget / 2)
+        tc, nc, rc = entry(cores, budget / 2)
+        return {"value": round(tc * 1e3, 1), "unit": "ms per prefill (gate+up+down, extrapolated)", "cores": cores,
+                "single_thread": round(t1 * 1e3, 1),
+                "matmul_gflop_per_s": round(total_flop / (tc * rc["matmul_s"] / (rc["dequant_s"] + rc["matmul_s"])) / 1e9, 1),
+                "sample": f"{nc} + {n1} expert projections of the 2048-token Zipf(1.1) top-{TOP_K} prefill "
+                          f"({routed.size} experts routed, {int(counts.sum())} pairs; {cores} threads, then 1)"}
+
+    budget = seconds / 5
+    head = decode_entry("iq2_ks", 1, 2 * budget)
+    configs = {"iq2_ks_1_token": head, "iq2_k_8_tokens": decode_entry("iq2_k", 8, budget),
+               "iq1_s_r4_1_token": decode_entry("iq1_s_r4", 1, budget), "zipf_prefill_2048": prefill_entry(budget)}
+    return {"value": head["value"], "unit": "GB/s", "cores": cores, "kind": kind,
+            "sample": head["sample"], "single_thread": head["single_thread"], "cpu_model": _cpu_model(),
+            "configs": configs}
 
 
 def prefill_launcher(torch, device, member: str, projection: str, kind: str, args, seed: int = 23):
@@ -827,6 +1013,8 @@ def main() -> int:
     step = results["iq2_ks"].pop("_step")
     head = headline(torch, step, args.steps, args.warmup)
     log(f"[headline] {args.steps} steps: {head['ms_per_step'] * 1e3:.2f} us/step, {head['gb_per_s']:.1f} GB/s")
+    if "module" in cells:
+        results["module"] = module_cell(torch, device, args, seed=41)
     if "iq2_k" in cells:
         results["iq2_k"] = decode_cell(torch, device, "iq2_k", 8, args, seed=13, windows=windows)
     if "iq1_s_r4" in cells:
@@ -869,6 +1057,8 @@ def main() -> int:
         for c, cell in (r.get("cells") or {}).items():
             key = f"{m}_{c}" + (f"_x{r['tokens']}" if r.get("tokens", 1) != 1 else "")
             summary[key] = {k: round(cell[k], 3) for k in ("x_floor", "x_stream", "x_floor_grid") if k in cell}
+            if "stream_best" in cell:
+                summary[key]["stream_best"] = cell["stream_best"]
             summary[key]["us"] = round(cell["decode"]["median_us"], 2)
             gates[key] = dict(cell["gates"])
             if "within_bar_vs_grid_floor" in cell:
@@ -878,6 +1068,8 @@ def main() -> int:
             key = f"producer_{m}_{c}"
             summary[key] = {"x_floor": round(cell["x_floor"], 3), "us": round(cell["decode"]["median_us"], 2)}
             gates[key] = cell["gates"]
+    if "module" in results:
+        summary["module_iq2_ks_x1"] = {k: results["module"][k]["median_us"] for k in ("gate", "down")}
     if "verify" in results:
         summary["verify"] = {k: {m: v[m]["median_us"] for m in ("pairs", "sorted", "union")}
                              for k, v in results["verify"].items() if k.startswith("tokens_")}

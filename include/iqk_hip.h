@@ -94,6 +94,13 @@ int iqk_gemv_floor_grid(int member, int64_t in_features, int64_t out_features, i
 // aligned, bytes a multiple of 16) with no expert-id read and no decode, and
 // writes a fold of them to out (u32 [ceil(bytes / 4096)], no meaningful values).
 int iqk_stream_floor(const void *src, uint64_t bytes, uint32_t *out, void *stream);
+// No counterpart either: the byte-stream floor with more bytes in flight --
+// each lane issues loads_per_lane (4, 8 or 16) 16-byte loads before folding
+// any, and at most max_waves wavefronts (0: one per chunk) stride over the
+// span in chunks of loads_per_lane KiB.  `out` holds one u32 per wavefront:
+// blocks of four wavefronts covering min(chunks, max_waves or chunks).
+int iqk_stream_floor_wide(const void *src, uint64_t bytes, int loads_per_lane, uint64_t max_waves, uint32_t *out,
+                          void *stream);
 
 // Decode GEMV over expert-sorted pairs, one workgroup per pair (replaces
 // gemv_sorted_kernel + IqkSwitchLinear.gemv_sorted,

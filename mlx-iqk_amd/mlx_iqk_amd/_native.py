@@ -38,6 +38,7 @@ SIGNATURES = {
     "iqk_gemv_floor_grid": (c_int, [c_int, c_int64, c_int64, c_int64, c_void_p, ctypes.POINTER(c_void_p), c_int,
                                     c_void_p, c_uint32, c_uint32, c_void_p, c_void_p]),
     "iqk_stream_floor": (c_int, [c_void_p, ctypes.c_uint64, c_void_p, c_void_p]),
+    "iqk_stream_floor_wide": (c_int, [c_void_p, ctypes.c_uint64, c_int, ctypes.c_uint64, c_void_p, c_void_p]),
     "iqk_gemv_sorted": (c_int, [c_int, c_int64, c_int64, c_int64, c_void_p, c_int64, ctypes.POINTER(c_void_p),
                                 c_int, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p]),
     "iqk_gemv_union": (c_int, [c_int, c_int64, c_int64, c_int64, c_void_p, c_int64, ctypes.POINTER(c_void_p),

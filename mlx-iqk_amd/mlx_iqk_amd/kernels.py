@@ -192,24 +192,45 @@ def gemv(member: str, x: torch.Tensor, streams: list[torch.Tensor], sel: torch.T
     return out
 
 
-def stream_floor(src: torch.Tensor, nbytes: int, out: torch.Tensor | None = None) -> torch.Tensor:
+def stream_floor_words(nbytes: int, loads: int = 4, max_waves: int = 0) -> int:
+    """Output words of :func:`stream_floor` for these arguments."""
+    if loads == 4 and not max_waves:
+        return (int(nbytes) + 4095) // 4096
+    chunks = (int(nbytes) + 1024 * loads - 1) // (1024 * loads)
+    waves = min(chunks, max_waves) if max_waves else chunks
+    return (waves + 3) // 4 * 4
+
+
+def stream_floor(src: torch.Tensor, nbytes: int, out: torch.Tensor | None = None, *, loads: int = 4,
+                 max_waves: int = 0) -> torch.Tensor:
     """The pure byte-stream floor: one dispatch reading the first ``nbytes`` of
     ``src`` (any contiguous GPU tensor, 16-byte aligned; ``nbytes`` a multiple of
     16), with no expert-id read and no decode.  Returns the dispatch's output
-    words (u32 ``[ceil(nbytes / 4096)]``, no meaningful values)."""
+    words (u32, :func:`stream_floor_words` of them, no meaningful values).
+
+    The default form has each wavefront read one 4 KiB chunk; ``loads`` (8 or
+    16) puts that many KiB in flight a wavefront, and ``max_waves`` caps the
+    wavefronts, which then stride over the span."""
     if not isinstance(src, torch.Tensor) or src.device.type != "cuda" or not src.is_contiguous():
         raise IqkKernelError("src must be a contiguous GPU tensor")
-    nbytes = int(nbytes)
+    nbytes, loads, max_waves = int(nbytes), int(loads), int(max_waves)
     if nbytes <= 0 or nbytes % 16 or nbytes > src.numel() * src.element_size():
         raise IqkKernelError(f"{nbytes} bytes is not a positive multiple of 16 within src")
-    words = (nbytes + 4095) // 4096
+    if loads not in (4, 8, 16) or max_waves < 0:
+        raise IqkKernelError(f"loads must be 4, 8 or 16 and max_waves >= 0, got {loads}, {max_waves}")
+    words = stream_floor_words(nbytes, loads, max_waves)
     if out is None:
         out = torch.empty(words, dtype=torch.int32, device=src.device)
     elif out.numel() < words or out.dtype not in (torch.int32, torch.uint32) or out.device != src.device:
         raise IqkKernelError(f"out must hold {words} 32-bit words on {src.device}")
-    rc = _native.load().iqk_stream_floor(src.data_ptr(), nbytes, out.data_ptr(), _stream_ptr(src.device))
+    lib = _native.load()
+    if loads == 4 and not max_waves:
+        rc = lib.iqk_stream_floor(src.data_ptr(), nbytes, out.data_ptr(), _stream_ptr(src.device))
+    else:
+        rc = lib.iqk_stream_floor_wide(src.data_ptr(), nbytes, loads, max_waves, out.data_ptr(),
+                                       _stream_ptr(src.device))
     if rc:
-        _native.check(rc, f"iqk_stream_floor({nbytes})")
+        _native.check(rc, f"iqk_stream_floor({nbytes}, loads={loads}, max_waves={max_waves})")
     return out
 
 

@@ -100,8 +100,8 @@ class IqkSwitchLinear(torch.nn.Module):
             self.register_buffer(name, torch.zeros(shape, dtype=dtypes[name], device=device))
         # the streams checked once for the launchers (kernels.CheckedStreams),
         # dropped whenever a stream is reassigned or the module moves, and
-        # re-checked whenever a stream's storage, shape or dtype differs from
-        # the record's (register_buffer and ``.data =`` bypass __setattr__)
+        # re-checked whenever a stream's address differs from the record's
+        # (register_buffer and ``.data =`` bypass __setattr__)
         object.__setattr__(self, "_stream_set", frozenset(self.stream_names()))
         object.__setattr__(self, "_checked_streams", None)
         object.__setattr__(self, "_checked_sig", None)
@@ -117,9 +117,11 @@ class IqkSwitchLinear(torch.nn.Module):
 
     def _checked(self) -> kernels.CheckedStreams:
         """The streams as the launchers take them, checked on first use and
-        again whenever a stream tensor's address, shape or dtype has changed."""
+        again whenever a stream's address differs from the record's (a new
+        tensor; one of another shape or dtype on the same address can only
+        be a view of the same storage, which stays allocated)."""
         streams = self._streams()
-        sig = tuple((t.data_ptr(), t.shape, t.stride(), t.dtype, t.device) for t in streams)
+        sig = tuple(t.data_ptr() for t in streams)
         if self._checked_streams is None or sig != self._checked_sig:
             object.__setattr__(self, "_checked_streams", kernels.CheckedStreams(
                 self.member, streams, self.num_experts, self.out_features, self.in_features))

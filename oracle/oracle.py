@@ -70,11 +70,19 @@ def row_bytes(member: str, n: int) -> int:
     return _ROW_BYTES[member](n)
 
 
-def dequantize(member: str, wire: np.ndarray, n: int) -> np.ndarray:
-    """Oracle float32 dequantization of ik wire rows ``[rows, row_bytes]``."""
+def _out(rows: int, n: int, out: np.ndarray | None) -> np.ndarray:
+    if out is None:
+        return np.empty((rows, n), dtype=np.float32)
+    assert out.dtype == np.float32 and out.shape == (rows, n) and out.flags.c_contiguous, (out.dtype, out.shape)
+    return out
+
+
+def dequantize(member: str, wire: np.ndarray, n: int, out: np.ndarray | None = None) -> np.ndarray:
+    """Oracle float32 dequantization of ik wire rows ``[rows, row_bytes]``
+    (into ``out`` when given)."""
     buf = np.ascontiguousarray(wire, dtype=np.uint8)
     assert buf.ndim == 2 and buf.shape[1] == row_bytes(member, n), (member, n, buf.shape)
-    out = np.empty((buf.shape[0], n), dtype=np.float32)
+    out = _out(buf.shape[0], n, out)
     rc = getattr(_load_oracle(), f"oracle_dequant_{member}")(
         buf.ctypes.data_as(ctypes.c_void_p), out.ctypes.data_as(_F32P), buf.shape[0], n)
     if rc != 0:
@@ -117,10 +125,11 @@ def ref_quantize(member: str, rows: np.ndarray, imatrix: np.ndarray | None) -> n
     return out
 
 
-def ref_dequantize(member: str, wire: np.ndarray, n: int) -> np.ndarray:
-    """The reference's own CPU dequantizer (compiled vendored source)."""
+def ref_dequantize(member: str, wire: np.ndarray, n: int, out: np.ndarray | None = None) -> np.ndarray:
+    """The reference's own CPU dequantizer (compiled vendored source), into
+    ``out`` when given."""
     buf = np.ascontiguousarray(wire, dtype=np.uint8)
-    out = np.empty((buf.shape[0], n), dtype=np.float32)
+    out = _out(buf.shape[0], n, out)
     rc = getattr(_load_ref(member), f"iqk_dequantize_{member}")(
         buf.ctypes.data_as(ctypes.c_void_p), out.ctypes.data_as(_F32P), buf.shape[0], n)
     if rc != 0:

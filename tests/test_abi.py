@@ -81,7 +81,11 @@ def test_entry_points_refuse_bad_arguments_before_launching(lib):
     assert lib.iqk_grouped_gemm(4096, 0, 4, 8, p, 8, p, p, p, None, p, None) == _native.ERR_GEOMETRY
     assert lib.iqk_grouped_gemm(4020, 2048, 4, 8, p, 8, p, p, p, None, p, None) == _native.ERR_GEOMETRY
     assert lib.iqk_grouped_gemm(4096, 2048, 4, 8, None, 8, p, p, p, None, p, None) == _native.ERR_ARGUMENT
+    assert lib.iqk_stream_floor_wide(p, 4096, 5, 0, p, None) == _native.ERR_ARGUMENT  # 4, 8 or 16 loads
+    assert lib.iqk_stream_floor_wide(p, 4100, 8, 0, p, None) == _native.ERR_ARGUMENT  # not whole 16-byte words
+    assert lib.iqk_stream_floor_wide(None, 4096, 8, 0, p, None) == _native.ERR_ARGUMENT
     # empty work is a no-op success, with no launch
+    assert lib.iqk_stream_floor_wide(p, 0, 8, 0, p, None) == 0
     assert lib.iqk_gemv(0, 4096, 2048, 256, p, streams, 5, p, 6, 0, p, None) == 0
     assert lib.iqk_grouped_gemm(4096, 2048, 0, 0, None, 0, None, None, None, None, None, None) == 0
     assert lib.iqk_hip_last_error() == 0

@@ -306,6 +306,41 @@ def test_floor_kernels_run(device, member, n):
     assert torch.isfinite(y.float()).all() and torch.isfinite(w.float()).all()
 
 
+def _stream_hash(words: np.ndarray, nbytes: int, loads: int, max_waves: int) -> np.ndarray:
+    """The byte-stream floor's output, restated: wavefront w folds its chunks
+    (``loads`` KiB each, every ``stride``-th) as sum over lanes and loads i of
+    (2i + 3)(x + 3y + 5z + 7w) of its 16-byte words, mod 2^32."""
+    u = np.zeros(((nbytes + 1024 * loads - 1) // (1024 * loads)) * 256 * loads, dtype=np.uint64)
+    u[:nbytes // 4] = words[:nbytes // 4]
+    q = u.reshape(-1, loads, 64, 4)  # chunk, load i, lane, word
+    coef = np.array([1, 3, 5, 7], dtype=np.uint64)
+    per_chunk = ((q * coef).sum(axis=3) * (2 * np.arange(loads, dtype=np.uint64) + 3)[None, :, None]).sum(axis=(1, 2))
+    chunks = per_chunk.size
+    waves = kernels.stream_floor_words(nbytes, loads, max_waves)
+    out = np.zeros(waves, dtype=np.uint64)
+    for c in range(chunks):  # the grid's wavefronts stride over the chunks
+        out[c % waves] += per_chunk[c]
+    return (out % (1 << 32)).astype(np.uint32)
+
+
+@pytest.mark.parametrize("loads,max_waves", [(4, 0), (8, 0), (16, 0), (16, 8), (8, 12), (4, 4)])
+def test_stream_floor_reads_every_byte(device, loads, max_waves):
+    """The byte-stream floor's output is a hash of every word it loaded (each
+    chunk exactly once, whichever wavefront took it), so matching the hash
+    restated on the CPU shows its load set is the span."""
+    rng = np.random.default_rng(loads * 100 + max_waves)
+    for nbytes in (16, 4096, 4096 * 5 + 48, 1 << 16, 3 * 16384 + 1024):
+        src = rng.integers(0, 1 << 32, size=(nbytes + 16 * 1024) // 4, dtype=np.uint64).astype(np.uint32)
+        got = kernels.stream_floor(torch.from_numpy(src.view(np.int32)).to(device), nbytes, loads=loads,
+                                   max_waves=max_waves)
+        got = got.cpu().numpy().view(np.uint32)
+        want = _stream_hash(src, nbytes, loads, max_waves)
+        if loads == 4 and not max_waves:
+            assert np.array_equal(got, want), nbytes
+        else:
+            assert np.array_equal(got[:want.size], want), (nbytes, loads, max_waves)
+
+
 # -- the grouped GEMM -----------------------------------------------------------------
 
 

@@ -53,7 +53,7 @@ def test_checked_streams_follow_buffers_replaced_behind_setattr(monkeypatch):
     third = m._checked()
     assert third is not second and third.ptrs[0] == m.qs.data_ptr()
 
-    m.scl.data = torch.zeros(m.scl.numel(), dtype=m.scl.dtype).view(m.scl.shape)
+    m.scl.data = torch.zeros(m.scl.numel(), dtype=m.scl.dtype).view(m.scl.shape)  # a new storage
     fourth = m._checked()
     assert fourth is not third and fourth.ptrs[1] == m.scl.data_ptr()
 
