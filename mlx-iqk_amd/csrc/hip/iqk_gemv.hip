@@ -299,7 +299,8 @@ int launch_gemv(int64_t n, const GemvArgs &a, uint32_t mats, hipStream_t st) {
 // The int8-MFMA path (iqk_gemv_mfma.hip); -1 when it does not apply.
 int gemv_mfma_dispatch(int floor, int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
                        int64_t n_x_rows, const void *const *streams, int n_streams, const uint32_t *sel,
-                       const uint32_t *toks, uint32_t pairs_per_row, uint32_t mats, void *y, hipStream_t st);
+                       const uint32_t *toks, bool union_runs, uint32_t pairs_per_row, uint32_t mats, void *y,
+                       hipStream_t st);
 
 // All GEMV entry points.  toks NULL: pair m reads x row m / pairs_per_row
 // (n_x_rows = mats / pairs_per_row); else x row toks[m] < n_x_rows (a row
@@ -310,7 +311,7 @@ int gemv_mfma_dispatch(int floor, int member, int64_t n, int64_t out, int64_t nu
 template <int FLOOR>
 int gemv_entry(int member, int64_t n, int64_t out, int64_t num_experts, const void *x, int64_t n_x_rows,
                const void *const *streams, int n_streams, const uint32_t *sel, const uint32_t *toks,
-               uint32_t pairs_per_row, uint32_t mats, void *y, void *stream) {
+               uint32_t pairs_per_row, uint32_t mats, void *y, void *stream, bool union_runs = false) {
     const int g = iqk_check_gemv_geometry(member, n, out);
     if (g != IQK_OK) return g;
     if (toks && member == IQK_MEMBER_IQ1_S_R4) return IQK_ERR_MEMBER;  // no sorted/union form
@@ -324,7 +325,7 @@ int gemv_entry(int member, int64_t n, int64_t out, int64_t num_experts, const vo
     if (mats > 65535u) return IQK_ERR_ARGUMENT;
     hipStream_t st = as_stream(stream);
     const int r = gemv_mfma_dispatch(FLOOR, member, n, out, num_experts, x, n_x_rows, streams, n_streams, sel,
-                                     toks, pairs_per_row, mats, y, st);
+                                     toks, union_runs, pairs_per_row, mats, y, st);
     if (r >= 0) return r;
     GemvArgs a;
     a.x = static_cast<const uint32_t *>(x);
@@ -389,17 +390,17 @@ int iqk_gemv_sorted(int member, int64_t n, int64_t out, int64_t num_experts, con
                                    1u, mats, y, stream);
 }
 
-// The union form is the sorted dispatch: a run of equal adjacent ids is a run
-// of adjacent workgroups, whose expert rows HBM delivers once (the rest of
-// the run reads them from L2).  Serializing a run's pairs in one workgroup,
-// the reference's formulation, measured slower on every routing tried.
+// The union form: adjacent pairs with one expert id share a workgroup, which
+// loads and expands the expert's rows once for them (see
+// gemv_mfma_union_kernel).  Where the int8-MFMA path does not apply (out not
+// a multiple of 32) it is the sorted dispatch.
 int iqk_gemv_union(int member, int64_t n, int64_t out, int64_t num_experts, const void *x, int64_t n_x_rows,
                    const void *const *streams, int n_streams, const uint32_t *sorted_ids, const uint32_t *toks,
                    uint32_t mats, void *y, void *stream) {
     if (member == IQK_MEMBER_IQ1_S_R4) return IQK_ERR_MEMBER;  // no union form
     if (!toks && mats) return IQK_ERR_ARGUMENT;
     return iqk::gemv_entry<0>(member, n, out, num_experts, x, n_x_rows, streams, n_streams, sorted_ids, toks,
-                                   1u, mats, y, stream);
+                                   1u, mats, y, stream, true);
 }
 
 }  // extern "C"

@@ -417,6 +417,52 @@ struct LaneIq2ks {
 #pragma unroll
         for (int r = 0; r < R; ++r) out[r] = acc[r] * half_bits_to_float(ln[r].dvb);
     }
+
+    // Pairs 0 .. np-1 (np <= PM, uniform per workgroup) of this lane's expert
+    // rows, each with its own activations (abase[p], sbs[p], nsbs[p] as for
+    // decode): each super-block's factors, pools and B operands are formed once
+    // and serve every pair, and each pair's MFMAs and folds are decode<1,
+    // true>'s in its order, so each pair's result is decode's bit for bit.
+    template <int PM>
+    __device__ __forceinline__ void decode_pairs(const uint8_t *const (&abase)[PM], const float *const (&sbs)[PM],
+                                                 const float *const (&nsbs)[PM], int np, int g,
+                                                 float (&out)[PM]) const {
+        const uint32_t g2 = uint32_t(g) | (uint32_t(g) << 8);
+        const uint32_t selg = (g2 | (g2 << 16)) + 0x04000400u;
+        const uint32_t hbg = hb >> (2 * g), abg = ab >> (2 * g);
+        float acc[PM];
+#pragma unroll
+        for (int p = 0; p < PM; ++p) acc[p] = 0.f;
+        uint32_t idx4 = 0;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int sp = s >> 1, t = s & 1;
+            if (t == 0) {
+                const uint32_t pb = perm(sc[2 * sp + 1], sc[2 * sp], selg);
+                const uint32_t u = hbg >> (16 * sp);
+                idx4 = (pb & 0x00000F0Fu) | ((pb >> 4) & 0x0F0F0000u) | ((u & 0x101u) << 4) | ((u & 0x202u) << 19);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {  // sub-block 8s + 2g + h: words 2h, 2h+1 of q[s]
+                const float idx5 = float((idx4 >> (8 * (2 * h + t))) & 0xffu);
+                const uint32_t m = uint32_t(int32_t(abg << (31 - (8 * s + h))) >> 31);
+                const uint32_t pool = (m & kV8Shift) | (~m & kV8Base);
+                const int4_t B0 = codes_to_i8(q[s][2 * h], pool), B1 = codes_to_i8(q[s][2 * h + 1], pool);
+#pragma unroll
+                for (int p = 0; p < PM; ++p) {
+                    if (p < np) {
+                        const float fac = fmaf(idx5, sbs[p][8 * s + 2 * g + h], nsbs[p][8 * s + 2 * g + h]);
+                        const uint8_t *ap = abase[p] + 256 * s + 32 * h;
+                        int4_t D = mfma(read_a_all(ap), B0, int4_t{0, 0, 0, 0});
+                        D = mfma(read_a_all(ap + 16), B1, D);
+                        acc[p] = fmaf(float(digits_sum(D)), fac, acc[p]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < PM; ++p) out[p] = acc[p] * half_bits_to_float(dvb);
+    }
 };
 
 // IQ2_K streams: qs u32 [N/16], scl u16 [N/64], sex u8 [N/128], dv f16 [N/256].
@@ -577,6 +623,59 @@ struct LaneIq2k {
             acc = fmaf(fmaf(2.f, sum, offs), dfac, acc);
         }
         return acc;
+    }
+
+    // Pairs 0 .. np-1 (np <= PM, uniform per workgroup) of this lane's expert
+    // rows, each with its own activations (abase[p], sbs[p], fw[p] as for
+    // decode): each super-block's pools and B operands are formed once and
+    // serve every pair, and each pair's factors, MFMAs and fold are
+    // decode<1, true>'s in its order, so each pair's result is decode's bit
+    // for bit.
+    template <int PM>
+    __device__ __forceinline__ void decode_pairs(const uint8_t *const (&abase)[PM], const float *const (&sbs)[PM],
+                                                 const float *const (&fw)[PM], const uint2_t *ktab, int np, int g,
+                                                 float (&out)[PM]) const {
+        const uint32_t selg = 0x01010000u + uint32_t(2 * g) * 0x01010101u;
+        const int exs = 8 * (g >> 1) + 4 * (g & 1);
+        const uint32_t scp[4] = {perm(sc0.y, sc0.x, selg), perm(sc0.w, sc0.z, selg), perm(sc1.y, sc1.x, selg),
+                                 perm(sc1.w, sc1.z, selg)};
+        const uint32_t exg[2] = {ex.x >> exs, ex.y >> exs};
+        float acc[PM];
+#pragma unroll
+        for (int p = 0; p < PM; ++p) acc[p] = 0.f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const float dvs = half_bits_to_float((dv[s >> 1] >> (16 * (s & 1))) & 0xffffu);
+            const uint32_t a8 = __umul24((exg[s >> 1] >> (16 * (s & 1))) & 15u, 0x204081u);
+            const uint32_t kofs =
+                ((scp[s] << 3) & 0x00780078u) | ((scp[s] >> 1) & 0x78007800u) | ((a8 & 0x01010101u) << 7);
+            int4_t B[4];
+            float ey[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint2_t e = *reinterpret_cast<const uint2_t *>(reinterpret_cast<const uint8_t *>(ktab) +
+                                                                     ((kofs >> (8 * j)) & 0xffu));
+                B[j] = codes_to_i8(q[s][j], e.x);
+                ey[j] = __uint_as_float(e.y);
+            }
+#pragma unroll
+            for (int p = 0; p < PM; ++p) {
+                if (p < np) {
+                    const float4 fwv = *reinterpret_cast<const float4 *>(fw[p] + 16 * s + 4 * g);
+                    const float dfac = dvs * sbs[p][4 * s + g];
+                    float offs = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) offs = fmaf(ey[j], fwv[j], offs);
+                    int4_t W = int4_t{0, 0, 0, 0};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) W = mfma(read_a_all(abase[p] + 256 * s + 16 * j), B[j], W);
+                    const float sum = fmaf(float(W.z), 65536.f, fmaf(float(W.y), 256.f, float(W.x)));
+                    acc[p] = fmaf(fmaf(2.f, sum, offs), dfac, acc[p]);
+                }
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < PM; ++p) out[p] = acc[p];
     }
 };
 
@@ -1009,6 +1108,133 @@ void gemv_mfma_pairs_kernel(Gemv2Args a) {
     }
 }
 
+// The union form (sorted pairs, IQ2 members; reference: the first pair of a
+// run of equal ids computes the run, src/mlx_iqk/kernels.py:484-572): a
+// workgroup serves a segment of up to PM adjacent pairs with one expert id.
+// Pair m starts a segment when m % PM == 0 or its id differs from pair
+// m - 1's; the segment runs on while the id repeats, up to the next multiple
+// of PM (so a workgroup decides from at most PM + 1 ids).  The segment's
+// expert rows are loaded and expanded once for all its pairs; each pair
+// stages its own activation row (a run's pairs are different tokens); the
+// workgroups of a segment's later pairs exit at once.  Every pair's output is
+// the pair GEMV's, bit for bit.
+template <int MEMBER, int N, int PM>
+struct GemvUnionSmem {
+    uint8_t dig[PM][3 * kPlaneStride<N>] __attribute__((aligned(16)));
+    uint8_t zero[kZeroSpan<MEMBER, N>] __attribute__((aligned(16)));  // what lanes without activations read
+    float sbs[PM][N / 32] __attribute__((aligned(16)));
+    float aux[PM][MEMBER == IQ2_KS ? N / 32 : N / 16] __attribute__((aligned(16)));  // nsbs (IQ2_KS), fw (IQ2_K)
+    float part[PM][Gemv2Shape<MEMBER, N>::KS][4][kGroupRows];
+    uint2_t ktab[MEMBER == IQ2_K ? 32 : 1];
+};
+
+template <int MEMBER, int N, int PM>
+__global__ __launch_bounds__((Gemv2Shape<MEMBER, N>::THREADS))
+__attribute__((amdgpu_waves_per_eu(6)))
+void gemv_mfma_union_kernel(Gemv2Args a) {
+    static_assert(MEMBER != IQ1_S_R4, "no union form for IQ1_S_R4");
+    using S = Gemv2Shape<MEMBER, N>;
+    constexpr int KS = S::KS;
+    constexpr int ROWS = kGroupRows;
+    __shared__ GemvUnionSmem<MEMBER, N, PM> sm;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, l = tid & 63;
+    const int n = l & 15, g = l >> 4;
+    const int kq = wave % KS, tile = wave / KS;
+    const uint32_t m0 = blockIdx.z;
+    const uint32_t rowg = blockIdx.x * ROWS;
+
+    // The segment (uniform): a later pair of a segment exits; a head counts
+    // the pairs after it with its id, up to the next multiple of PM.
+    const uint32_t e_raw = a.sel[m0];
+    if (m0 % PM != 0 && a.sel[m0 - 1] == e_raw) return;
+    int np = 1;
+#pragma unroll
+    for (int p = 1; p < PM; ++p)
+        if (np == p && m0 + p < a.mats && (m0 + p) % PM != 0 && a.sel[m0 + p] == e_raw) np = p + 1;
+    uint32_t tok[PM];
+#pragma unroll
+    for (int p = 0; p < PM; ++p) tok[p] = p < np ? a.toks[m0 + uint32_t(p)] : 0u;
+    // an id beyond the stack reads expert 0 (in bounds) and writes NaN rows; a
+    // row beyond x reads row 0 and writes NaN
+    const bool valid = e_raw < a.num_experts;
+    const uint32_t e = valid ? e_raw : 0u;
+
+    // activation loads first (they do not wait for the expert's rows)
+    const bool stager = tid < S::UNITS;  // uniform per wavefront
+    uint4_t xv[PM];
+#pragma unroll
+    for (int p = 0; p < PM; ++p) {
+        xv[p] = uint4_t{0u, 0u, 0u, 0u};
+        if (p < np && stager)
+            xv[p] = load_u4(bytes(a.x) + ((tok[p] < a.n_x_rows ? tok[p] : 0u) * (2 * N) + 16 * uint32_t(tid)));
+    }
+    constexpr bool KTAB = MEMBER == IQ2_K;
+    uint2_t ktv = {0u, 0u};
+    if (KTAB && tid < 32) ktv = reinterpret_cast<const uint2_t *>(kIq2kTab.w)[tid];
+    LaneOf<MEMBER, N> lane;  // rows rowg + 16 tile + n of the segment's expert
+    lane.load(a, e * a.out_features + rowg + 16 * tile + n, kq, g);
+
+    if (KTAB && tid < 32) sm.ktab[tid] = ktv;
+    if (tid < kZeroSpan<MEMBER, N> / 16) reinterpret_cast<uint4_t *>(sm.zero)[tid] = uint4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int p = 0; p < PM; ++p)
+        if (p < np && stager)
+            stage_activations<N, true, 0, kExpBlock<MEMBER>>(sm.dig[p], sm.sbs[p],
+                                                             MEMBER == IQ2_KS ? sm.aux[p] : nullptr, nullptr,
+                                                             MEMBER == IQ2_K ? sm.aux[p] : nullptr, tid, xv[p]);
+    __syncthreads();
+    const int ai = l & 15;  // this lane's A row
+    const bool data = (ai >> 2) == g && (ai & 3) < 3;
+    const uint8_t *abase[PM];
+    const float *sbs[PM], *aux[PM];
+#pragma unroll
+    for (int p = 0; p < PM; ++p) {
+        abase[p] = data ? sm.dig[p] + (ai & 3) * kPlaneStride<N> + S::WK * kq + 64 * g : sm.zero;
+        sbs[p] = sm.sbs[p] + (S::WK / kExpBlock<MEMBER>) * kq;
+        aux[p] = sm.aux[p] + (S::WK / (MEMBER == IQ2_KS ? 32 : 16)) * kq;
+    }
+    float acc[PM];
+    if constexpr (MEMBER == IQ2_KS)
+        lane.template decode_pairs<PM>(abase, sbs, aux, np, g, acc);
+    else
+        lane.template decode_pairs<PM>(abase, sbs, aux, sm.ktab, np, g, acc);
+#pragma unroll
+    for (int p = 0; p < PM; ++p)
+        if (p < np) sm.part[p][kq][g][16 * tile + n] = acc[p];
+    __syncthreads();
+    if (tid < ROWS * np) {
+        const int p = tid / ROWS, row = tid % ROWS;
+        float sum = 0.f;
+#pragma unroll
+        for (int k = 0; k < KS; ++k)
+            sum += (sm.part[p][k][0][row] + sm.part[p][k][1][row]) + (sm.part[p][k][2][row] + sm.part[p][k][3][row]);
+        bool x_ok = false;
+#pragma unroll
+        for (int q = 0; q < PM; ++q)
+            if (q == p) x_ok = tok[q] < a.n_x_rows;
+        a.y[size_t(m0 + uint32_t(p)) * a.out_features + rowg + uint32_t(row)] =
+            valid && x_ok ? uint16_t(float_to_half_bits(sum)) : kHalfNaN;
+    }
+}
+
+// Pairs a union workgroup serves at most.  A pair's staged activations take
+// 12.3 KB of LDS (4096 wide), so three pairs keep three workgroups a CU.
+constexpr int kUnionPairs = 3;
+
+template <int MEMBER>
+int launch_union(int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t st) {
+    const dim3 grid{a.out_features / kGroupRows, 1u, mats};
+    if (n == 4096)
+        hipLaunchKernelGGL((gemv_mfma_union_kernel<MEMBER, 4096, kUnionPairs>), grid,
+                           dim3{uint32_t(Gemv2Shape<MEMBER, 4096>::THREADS)}, 0, st, a);
+    else
+        hipLaunchKernelGGL((gemv_mfma_union_kernel<MEMBER, 2048, kUnionPairs>), grid,
+                           dim3{uint32_t(Gemv2Shape<MEMBER, 2048>::THREADS)}, 0, st, a);
+    return record_launch(hipGetLastError());
+}
+
 template <int MEMBER, int FLOOR, int MODE, int R, int P>
 int launch_gemv_mfma(int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t st) {
     const uint32_t groups = a.out_features / (kGroupRows * R);
@@ -1079,11 +1305,12 @@ int pairs_per_group(uint64_t workgroups, uint32_t pairs_per_row) {
 // Called by the GEMV entry points (after their argument checks) when
 // out_features is a multiple of the workgroup's 32 rows; returns -1 when this
 // path does not apply.  `toks` NULL = pairs mode (x row m / pairs_per_row);
-// else x row toks[m] of n_x_rows (the sorted and union entry points, one
-// dispatch: see GemvMode).
+// else x row toks[m] of n_x_rows: the sorted entry point (see GemvMode), or
+// with union_runs the union kernel.
 int gemv_mfma_dispatch(int floor, int member, int64_t n, int64_t out, int64_t num_experts, const void *x,
                        int64_t n_x_rows, const void *const *streams, int n_streams, const uint32_t *sel,
-                       const uint32_t *toks, uint32_t pairs_per_row, uint32_t mats, void *y, hipStream_t st) {
+                       const uint32_t *toks, bool union_runs, uint32_t pairs_per_row, uint32_t mats, void *y,
+                       hipStream_t st) {
     if (out % kGroupRows) return -1;
     // 32-bit offsets: every stream (the code plane is the largest, N/4 bytes a
     // row) and the activations stay below 4 GiB
@@ -1125,6 +1352,13 @@ int gemv_mfma_dispatch(int floor, int member, int64_t n, int64_t out, int64_t nu
         }
     }
     if (floor != kDecode) return IQK_ERR_ARGUMENT;
+    if (union_runs) {
+        switch (member) {
+            case IQK_MEMBER_IQ2_KS: return launch_union<IQ2_KS>(n, a, mats, st);
+            case IQK_MEMBER_IQ2_K: return launch_union<IQ2_K>(n, a, mats, st);
+            default: return IQK_ERR_MEMBER;  // no union form for IQ1_S_R4
+        }
+    }
     return launch_member<kDecode, kSorted, 1>(member, n, a, mats, st);
 }
 

@@ -251,9 +251,10 @@ def gemv_sorted(member: str, x: torch.Tensor, streams: list[torch.Tensor], sorte
     fp16 ``[mats, out]``; each element equals :func:`gemv`'s for the same
     (expert, activation row), bit for bit.  ``union=True`` is the union entry
     point (the multi-token verify shape, src/mlx_iqk/kernels.py:484-578),
-    otherwise the sorted one (src/mlx_iqk/kernels.py:404-482); both run one
-    workgroup per pair, a run's adjacent workgroups sharing its expert's rows
-    through L2.  IQ2 members only.
+    otherwise the sorted one (src/mlx_iqk/kernels.py:404-482).  The sorted
+    form runs one workgroup per pair; the union form gives up to three
+    adjacent pairs of one expert a workgroup, which loads and expands the
+    expert's rows once for them.  IQ2 members only.
     """
     check_iq2_member(member)
     n = int(x.shape[-1])

@@ -246,13 +246,12 @@ class IqkSwitchLinear(torch.nn.Module):
                                    self.out_features)
 
     def gemv_union(self, x: torch.Tensor, sorted_ids: torch.Tensor, toks: torch.Tensor) -> torch.Tensor:
-        """:meth:`gemv_sorted` reading each distinct expert from HBM once per
-        run of equal adjacent ids: the multi-token verify shape, where several
-        pairs select one expert (reference: src/mlx_iqk/nn.py:301-333).  Output
-        and arithmetic identical to :meth:`gemv_sorted`, and the same
-        dispatch: a run's pairs are adjacent workgroups that share the
-        expert's rows through L2.  The caller applies the inverse
-        permutation."""
+        """:meth:`gemv_sorted` decoding each run of equal adjacent ids
+        together: the multi-token verify shape, where several pairs select one
+        expert (reference: src/mlx_iqk/nn.py:301-333).  Output identical to
+        :meth:`gemv_sorted` bit for bit; up to three adjacent pairs of one
+        expert share a workgroup, which loads and expands the expert's rows
+        once for them.  The caller applies the inverse permutation."""
         xt, sel, tok = self._sorted_operands(x, sorted_ids, toks)
         return kernels.gemv_sorted(self.member, xt, self._checked(), sel, tok, self.num_experts,
                                    self.out_features, union=True)
