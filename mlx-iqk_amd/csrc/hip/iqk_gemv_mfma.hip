@@ -868,13 +868,21 @@ enum GemvMode : int {
 // IQ1_S_R4, and the IQ2 members at 2048 wide): each wavefront takes 32 rows, two MFMA column blocks that
 // share every A read, so a workgroup stages its activations for 64 rows;
 // five wavefronts per SIMD.
-template <int MEMBER, int N, int FLOOR, int MODE, int R>
-__global__ __launch_bounds__((Gemv2Shape<MEMBER, N>::THREADS))
+// T: 16-row tiles a workgroup (2: 32 rows; 1: 16 rows, for dispatches too
+// small to give every CU the same number of 32-row workgroups, such as one
+// token's gate alone: 384 of them on 256 CUs).  With T = 1 each thread
+// stages two activation units (N = 4096) and expands twice the grid entries.
+template <int MEMBER, int N, int FLOOR, int MODE, int R, int T = 2>
+__global__ __launch_bounds__((64 * T * Gemv2Shape<MEMBER, N>::KS))
 __attribute__((amdgpu_waves_per_eu(R == 2 ? 5 : 6)))
 void gemv_mfma_kernel(Gemv2Args a) {
     using S = Gemv2Shape<MEMBER, N>;
     constexpr int KS = S::KS;
-    constexpr int ROWS = kGroupRows * R;  // rows per workgroup
+    constexpr int THREADS = 64 * T * KS;
+    constexpr int ROWS = 16 * T * R;  // rows per workgroup
+    constexpr int XU = S::UNITS > THREADS ? S::UNITS / THREADS : 1;  // activation units a thread stages
+    static_assert(T == 1 || T == 2, "one or two 16-row tiles");
+    static_assert(S::UNITS <= THREADS || S::UNITS == XU * THREADS, "whole staging passes");
     __shared__ Gemv2Smem<MEMBER, N, R, 1> sm;
 
     const int tid = threadIdx.x;
@@ -892,14 +900,33 @@ void gemv_mfma_kernel(Gemv2Args a) {
     // expert id, and vector loads retire in order, so staging them waits for
     // none of the stream bytes issued after them.
     const bool stager = tid < S::UNITS;  // uniform per wavefront
-    uint4_t xv = {0u, 0u, 0u, 0u};         // fp16 pairs 4tid .. 4tid+3 of the pair's row
-    if (stager) xv = load_u4(bytes(a.x) + ((x_ok ? tok : 0u) * (2 * N) + 16 * uint32_t(tid)));
+    uint4_t xv[XU];                        // fp16 pairs 4u .. 4u+3 of the pair's row, unit u = tid + THREADS i
+#pragma unroll
+    for (int i = 0; i < XU; ++i) {
+        xv[i] = uint4_t{0u, 0u, 0u, 0u};
+        if (stager)
+            xv[i] = load_u4(bytes(a.x) + ((x_ok ? tok : 0u) * (2 * N) + 16 * uint32_t(tid + THREADS * i)));
+    }
     constexpr bool IQ1 = MEMBER == IQ1_S_R4;
-    // IQ1_S_R4: the codes of grid entries 4tid .. 4tid+3
+    // IQ1_S_R4: the codes of grid entries 4u .. 4u+3, u = tid + THREADS i
     constexpr bool GRID = IQ1 && FLOOR != kFloor;
-    static_assert(!IQ1 || IQK_IQ1S_GRID_SIZE == 4 * S::THREADS, "four grid entries per thread");
-    uint2_t gridc = {0u, 0u};
-    if constexpr (GRID) gridc = reinterpret_cast<const uint2_t *>(iqk_iq1s_grid_codes)[tid];
+    constexpr int GU = IQK_IQ1S_GRID_SIZE / (4 * THREADS);  // four-entry units a thread expands
+    static_assert(!IQ1 || IQK_IQ1S_GRID_SIZE == 4 * GU * THREADS, "whole grid units per thread");
+    uint2_t gridc[IQ1 ? GU : 1] = {};
+    if constexpr (GRID) {
+#pragma unroll
+        for (int i = 0; i < GU; ++i) gridc[i] = reinterpret_cast<const uint2_t *>(iqk_iq1s_grid_codes)[tid + THREADS * i];
+    }
+    const auto stage_grid = [&]() {
+#pragma unroll
+        for (int i = 0; i < (IQ1 ? GU : 1); ++i) {
+            uint4_t g0, g1;
+            expand_grid_pair(gridc[i].x, g0);
+            expand_grid_pair(gridc[i].y, g1);
+            reinterpret_cast<uint4_t *>(sm.b8)[2 * (tid + THREADS * i)] = g0;
+            reinterpret_cast<uint4_t *>(sm.b8)[2 * (tid + THREADS * i) + 1] = g1;
+        }
+    };
     constexpr bool KTAB = MEMBER == IQ2_K && FLOOR == kDecode;
     uint2_t ktv = {0u, 0u};
     if (KTAB && tid < 32) ktv = reinterpret_cast<const uint2_t *>(kIq2kTab.w)[tid];
@@ -918,15 +945,13 @@ void gemv_mfma_kernel(Gemv2Args a) {
     {
         float acc[R];
         if constexpr (FLOOR != kDecode) {
-            uint32_t h = xv.x + 3u * xv.y + 5u * xv.z + 7u * xv.w;
+            uint32_t h = 0;
+#pragma unroll
+            for (int i = 0; i < XU; ++i) h += xv[i].x + 3u * xv[i].y + 5u * xv[i].z + 7u * xv[i].w;
 #pragma unroll
             for (int r = 0; r < R; ++r) h += lane[r].hash();
             if constexpr (GRID) {  // kFloorGrid: the grid staging and every lookup
-                uint4_t g0, g1;
-                expand_grid_pair(gridc.x, g0);
-                expand_grid_pair(gridc.y, g1);
-                reinterpret_cast<uint4_t *>(sm.b8)[2 * tid] = g0;
-                reinterpret_cast<uint4_t *>(sm.b8)[2 * tid + 1] = g1;
+                stage_grid();
                 __syncthreads();
 #pragma unroll
                 for (int r = 0; r < R; ++r) h += lane[r].grid_hash(sm.b8);
@@ -935,19 +960,19 @@ void gemv_mfma_kernel(Gemv2Args a) {
             for (int r = 0; r < R; ++r) acc[r] = float((h >> r) & 0xffu);
         } else {
             {
-                if constexpr (GRID) {
-                    uint4_t g0, g1;
-                    expand_grid_pair(gridc.x, g0);
-                    expand_grid_pair(gridc.y, g1);
-                    reinterpret_cast<uint4_t *>(sm.b8)[2 * tid] = g0;
-                    reinterpret_cast<uint4_t *>(sm.b8)[2 * tid + 1] = g1;
-                }
+                if constexpr (GRID) stage_grid();
                 if (KTAB && tid < 32) sm.ktab[tid] = ktv;
             }
-            if (stager)
+            if (stager) {
                 stage_activations<N, !IQ1, kZeroSpan<MEMBER, N>, kExpBlock<MEMBER>>(
                     sm.dig, sm.sbs, MEMBER == IQ2_KS ? sm.nsbs : nullptr, IQ1 ? sm.fsum : nullptr,
-                    MEMBER == IQ2_K ? sm.fw : nullptr, tid, xv);
+                    MEMBER == IQ2_K ? sm.fw : nullptr, tid, xv[0]);
+#pragma unroll
+                for (int i = 1; i < XU; ++i)  // a quad's threads take units of one quad, so the DPP stays in it
+                    stage_activations<N, !IQ1, 0, kExpBlock<MEMBER>>(
+                        sm.dig, sm.sbs, MEMBER == IQ2_KS ? sm.nsbs : nullptr, IQ1 ? sm.fsum : nullptr,
+                        MEMBER == IQ2_K ? sm.fw : nullptr, tid + THREADS * i, xv[i]);
+            }
             __syncthreads();
             const int ai = l & 15;  // this lane's A row
             const bool data = (ai >> 2) == g && (ai & 3) < 3;
@@ -1235,37 +1260,39 @@ int launch_union(int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t st) {
     return record_launch(hipGetLastError());
 }
 
-template <int MEMBER, int FLOOR, int MODE, int R, int P>
+template <int MEMBER, int FLOOR, int MODE, int R, int P, int T = 2>
 int launch_gemv_mfma(int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t st) {
-    const uint32_t groups = a.out_features / (kGroupRows * R);
+    const uint32_t groups = a.out_features / (16 * T * R);
     const dim3 grid = MODE == kPairs ? dim3{groups, a.pairs_per_row / P, mats / a.pairs_per_row} : dim3{groups, 1u, mats};
-    const dim3 block4096{uint32_t(Gemv2Shape<MEMBER, 4096>::THREADS)}, block2048{uint32_t(Gemv2Shape<MEMBER, 2048>::THREADS)};
-    static_assert(P == 1 || (MODE == kPairs && R == 1), "several pairs a workgroup: pairs mode, one row block");
+    const dim3 block4096{uint32_t(64 * T * Gemv2Shape<MEMBER, 4096>::KS)},
+        block2048{uint32_t(64 * T * Gemv2Shape<MEMBER, 2048>::KS)};
+    static_assert(P == 1 || (MODE == kPairs && R == 1 && T == 2), "several pairs a workgroup: pairs mode, one row block");
     if constexpr (P > 1) {
         if (n == 4096)
             hipLaunchKernelGGL((gemv_mfma_pairs_kernel<MEMBER, 4096, FLOOR, P>), grid, block4096, 0, st, a);
         else
             hipLaunchKernelGGL((gemv_mfma_pairs_kernel<MEMBER, 2048, FLOOR, P>), grid, block2048, 0, st, a);
     } else if (n == 4096) {
-        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 4096, FLOOR, MODE, R>), grid, block4096, 0, st, a);
+        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 4096, FLOOR, MODE, R, T>), grid, block4096, 0, st, a);
     } else {
-        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 2048, FLOOR, MODE, R>), grid, block2048, 0, st, a);
+        hipLaunchKernelGGL((gemv_mfma_kernel<MEMBER, 2048, FLOOR, MODE, R, T>), grid, block2048, 0, st, a);
     }
     return record_launch(hipGetLastError());
 }
 
-template <int FLOOR, int MODE, int R, int P = 1>
+template <int FLOOR, int MODE, int R, int P = 1, int T = 2>
 int launch_member(int member, int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t st) {
     switch (member) {
-        case IQK_MEMBER_IQ2_KS: return launch_gemv_mfma<IQ2_KS, FLOOR, MODE, R, P>(n, a, mats, st);
-        case IQK_MEMBER_IQ2_K: return launch_gemv_mfma<IQ2_K, FLOOR, MODE, R, P>(n, a, mats, st);
+        case IQK_MEMBER_IQ2_KS: return launch_gemv_mfma<IQ2_KS, FLOOR, MODE, R, P, T>(n, a, mats, st);
+        case IQK_MEMBER_IQ2_K: return launch_gemv_mfma<IQ2_K, FLOOR, MODE, R, P, T>(n, a, mats, st);
         default:
-            if constexpr (MODE == kPairs) return launch_gemv_mfma<IQ1_S_R4, FLOOR, MODE, R, P>(n, a, mats, st);
+            if constexpr (MODE == kPairs) return launch_gemv_mfma<IQ1_S_R4, FLOOR, MODE, R, P, T>(n, a, mats, st);
             return IQK_ERR_MEMBER;  // no sorted or union form for IQ1_S_R4
     }
 }
 
-// A decode launch in pairs mode: R row blocks a wavefront, P pairs a workgroup.
+// A decode launch in pairs mode: R row blocks a wavefront, P pairs a
+// workgroup; pairs == 0 asks for 16-row workgroups (one pair, one row block).
 template <int FLOOR, int R>
 int launch_pairs(int member, int64_t n, const Gemv2Args &a, uint32_t mats, int pairs, hipStream_t st) {
     if constexpr (R != 1) {
@@ -1274,6 +1301,7 @@ int launch_pairs(int member, int64_t n, const Gemv2Args &a, uint32_t mats, int p
         switch (pairs) {
             case 3: return launch_member<FLOOR, kPairs, 1, 3>(member, n, a, mats, st);
             case 2: return launch_member<FLOOR, kPairs, 1, 2>(member, n, a, mats, st);
+            case 0: return launch_member<FLOOR, kPairs, 1, 1, 1>(member, n, a, mats, st);
             default: return launch_member<FLOOR, kPairs, 1, 1>(member, n, a, mats, st);
         }
     }
@@ -1297,7 +1325,16 @@ constexpr uint64_t kTwoRowMinGroupsIq2 = 8 * 768;
 // pairs a workgroup measured the same or slower.
 constexpr uint64_t kSharedStagingMinGroups = 2 * 768;
 
+// Dispatches of fewer 32-row workgroups than this (one round of three a CU)
+// run 16-row workgroups instead, so the CUs share the work evenly: one
+// token's gate alone (the switch module's own dispatch, 384 workgroups of 32
+// rows) gives 256 CUs one or two workgroups each.
+constexpr uint64_t kHalfTileMaxGroups = 768;
+
+// Pairs a workgroup: 3 or 2 (shared staging), 1, or 0 (one pair in 16-row
+// workgroups).
 int pairs_per_group(uint64_t workgroups, uint32_t pairs_per_row) {
+    if (workgroups < kHalfTileMaxGroups) return 0;
     if (workgroups < kSharedStagingMinGroups) return 1;
     return pairs_per_row % 3 == 0 ? 3 : pairs_per_row % 2 == 0 ? 2 : 1;
 }

@@ -186,6 +186,31 @@ def test_gemv_large_dispatch_equals_small_dispatches(device, member, n, top_k):
     assert np.all(np.isnan(yf[sel >= EXPERTS])) and np.all(np.isfinite(yf[sel < EXPERTS])), member
 
 
+@pytest.mark.parametrize("member", fmt.MEMBERS)
+@pytest.mark.parametrize("n", kernels.SUPPORTED_IN_FEATURES)
+def test_gemv_half_tile_dispatch_equals_full_tiles(device, member, n):
+    """Dispatches of fewer than 768 row workgroups of 32 rows run 16-row
+    workgroups (each thread stages two activation units, IQ1_S_R4 expands
+    twice the grid entries); between 768 and 1536 they run the 32-row,
+    one-pair form.  A row's arithmetic is the same in both, so the same pairs
+    give the same bits either way, and meet the float64 gate."""
+    print(f"gemv half tiles {member} n={n}", flush=True)
+    out, tokens, top_k = 256, 40, 3  # 120 pairs x 8 = 960 workgroups of 32 rows; a token alone: 24
+    _, streams, ref = _case(member, n, wirepack.seed_for(member, n, "half"), device, out=out)
+    rng = np.random.default_rng(29)
+    x = rng.standard_normal((tokens, n)).astype(np.float16)
+    sel = rng.integers(0, EXPERTS, size=tokens * top_k).astype(np.int32)
+    xt, st = torch.from_numpy(x).to(device), torch.from_numpy(sel).to(device)
+    full = kernels.gemv(member, xt, streams, st, top_k, EXPERTS, out).cpu().numpy()
+    half = np.concatenate([kernels.gemv(member, xt[t:t + 1], streams, st[t * top_k:(t + 1) * top_k], top_k,
+                                        EXPERTS, out).cpu().numpy() for t in range(tokens)])
+    assert np.array_equal(full.view(np.uint16), half.view(np.uint16)), member
+    _check_gemv(half, oracle.gemv_reference(ref, sel, x, top_k), (member, n))
+    for floor in (True, "grid"):
+        yf = kernels.gemv(member, xt[:1], streams, st[:top_k], top_k, EXPERTS, out, floor=floor)
+        assert torch.isfinite(yf.float()).all()
+
+
 @pytest.mark.parametrize("case", range(8))
 def test_gemv_dispatch_forms_agree_on_random_shapes(device, case):
     """Seeded random geometry and routing: member, width, 256-512 rows, 2-8
