@@ -92,8 +92,8 @@ def parse() -> argparse.Namespace:
                          f"{PROBE_COPY_BYTES >> 20} MiB (the HBM-byte calibration), and exit")
     ap.add_argument("--probe-kernel", default="decode:iq2_ks:1:gate_up",
                     help="decode|floor|floor_grid:<member>:<tokens>:gate_up|down, or fused|producer|gemm:<member>:"
-                         "gate|down (the 2048-token Zipf prefill), or pairs|sorted:<member>:<tokens>:<pool> (the "
-                         "verify shape: every token's top-6 from a pool of experts, gate geometry)")
+                         "gate|down (the 2048-token Zipf prefill), or pairs|sorted|union:<member>:<tokens>:<pool> "
+                         "(the verify shape: every token's top-6 from a pool of experts, gate geometry)")
     return ap.parse_args()
 
 
@@ -941,7 +941,7 @@ def probe(torch, device, args) -> int:
 
     kind, member, *rest = args.probe_kernel.split(":")
     info = {"probe": args.probe, "kernel": args.probe_kernel}
-    if kind in ("pairs", "sorted"):
+    if kind in ("pairs", "sorted", "union"):
         from mlx_iqk_amd import kernels, synth
         tokens, pool = int(rest[0]), int(rest[1])
         out, n = GU
@@ -959,7 +959,8 @@ def probe(torch, device, args) -> int:
                 kernels.gemv(member, x, stack, torch.from_numpy(flat).to(device), TOP_K, EXPERTS, out)
             else:
                 kernels.gemv_sorted(member, x, stack, torch.from_numpy(flat[order]).to(device),
-                                    torch.from_numpy((order // TOP_K).astype(np.int32)).to(device), EXPERTS, out)
+                                    torch.from_numpy((order // TOP_K).astype(np.int32)).to(device), EXPERTS, out,
+                                    union=kind == "union")
         info["pair_bytes_per_dispatch"] = tokens * TOP_K * out * ik_row_bytes(member, n)
         info["distinct_bytes_per_dispatch_mean"] = statistics.mean(distinct) * out * ik_row_bytes(member, n)
     elif kind in ("decode", "floor", "floor_grid"):

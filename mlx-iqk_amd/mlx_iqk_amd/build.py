@@ -15,6 +15,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 import tempfile
 from pathlib import Path
 
@@ -26,6 +27,7 @@ LIBDIR = PACKAGE / "_lib"
 
 CODEC_LIB = LIBDIR / "libiqk_codec.so"
 HIP_LIB = LIBDIR / "libiqk_hip.so"
+LAUNCH_EXT = LIBDIR / ("_iqk_launch" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
 
 # Source -> extra hipcc flags.  The MFMA decode GEMV folds each accumulator
 # right after its MFMA chain, so its MFMA results go straight to VGPRs.
@@ -122,9 +124,26 @@ def build_hip() -> Path:
     return HIP_LIB
 
 
+def launch_command(out: Path = LAUNCH_EXT, source_hash: str = "") -> list[str]:
+    """The CPython binding of the decode launch path, linked against the
+    kernel library beside it (found through $ORIGIN)."""
+    return ["gcc", "-O2", "-shared", "-fPIC", f"-I{sysconfig.get_paths()['include']}", f"-I{INCLUDE}",
+            f'-DIQK_SOURCE_HASH="{source_hash or hip_source_hash()}"', "-o", str(out),
+            str(CSRC / "launch" / "iqk_launch.c"), f"-L{LIBDIR}", "-liqk_hip", "-Wl,-rpath,$ORIGIN"]
+
+
+def build_launch() -> Path:
+    LIBDIR.mkdir(parents=True, exist_ok=True)
+    tmp = LAUNCH_EXT.with_suffix(".so.tmp")
+    _run(launch_command(tmp))
+    tmp.replace(LAUNCH_EXT)
+    return LAUNCH_EXT
+
+
 def build_all() -> None:
     build_codec()
     build_hip()
+    build_launch()
 
 
 if __name__ == "__main__":

@@ -15,6 +15,8 @@ refused before anything launches.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _native
@@ -125,21 +127,27 @@ class CheckedStreams:
     one whenever a stream's address, shape, strides or dtype differ from the
     ones it was made from)."""
 
-    __slots__ = ("key", "device", "ptrs", "count")
+    __slots__ = ("key", "device", "ptrs", "ptrs_addr", "count", "gemv_ok")
 
     def __init__(self, member: str, streams: list[torch.Tensor], num_experts: int, out_features: int,
                  in_features: int):
         self.device = check_streams(member, streams, num_experts, out_features, in_features)
         self.key = (member, int(num_experts), int(out_features), int(in_features))
         self.ptrs = _native.pointer_array([t.data_ptr() for t in streams])
+        self.ptrs_addr = ctypes.addressof(self.ptrs)
         self.count = len(streams)
+        try:  # a geometry the decode GEMV serves: its launches skip the check
+            check_gemv_geometry(in_features, out_features)
+            self.gemv_ok = True
+        except (IqkKernelError, ValueError):
+            self.gemv_ok = False
 
 
 def _streams_for(member: str, streams, num_experts: int, out_features: int, in_features: int):
     """The device, pointer array and count of a launch's streams: a
     CheckedStreams of this geometry as is, a list checked now."""
     if isinstance(streams, CheckedStreams):
-        if streams.key != (member, int(num_experts), int(out_features), int(in_features)):
+        if streams.key != (member, num_experts, out_features, in_features):
             raise IqkKernelError(f"streams checked for {streams.key}, used for "
                                  f"{(member, num_experts, out_features, in_features)}")
         return streams.device, streams.ptrs, streams.count
@@ -156,12 +164,15 @@ def gemv(member: str, x: torch.Tensor, streams: list[torch.Tensor], sel: torch.T
     GPU.  ``floor=True`` runs the deleted-decode floor instead, ``floor="grid"``
     that floor with IQ1_S_R4's grid lookups kept (the reference's IQ1 floor).
     """
-    check_member(member)
-    n = int(x.shape[-1])
-    check_gemv_geometry(n, out_features)
+    n = x.shape[-1]
+    if not (isinstance(streams, CheckedStreams) and streams.gemv_ok and streams.key[3] == n):
+        check_member(member)
+        check_gemv_geometry(n, out_features)
     device, ptrs, n_streams = _streams_for(member, streams, num_experts, out_features, n)
-    _require_cuda(x, "x", torch.float16, device)
-    _require_cuda(sel, "sel", (torch.int32, torch.uint32), device)
+    if not (x.dtype == torch.float16 and x.device == device and x.is_contiguous()):
+        _require_cuda(x, "x", torch.float16, device)
+    if not (sel.dtype == torch.int32 and sel.device == device and sel.is_contiguous()):
+        _require_cuda(sel, "sel", (torch.int32, torch.uint32), device)
     if x.dim() != 2 or sel.dim() != 1:
         raise IqkKernelError("x must be [rows, in_features] and sel [mats]")
     mats = int(sel.numel())
@@ -177,16 +188,21 @@ def gemv(member: str, x: torch.Tensor, streams: list[torch.Tensor], sel: torch.T
     if mats == 0:
         return out
     lib = _native.load()
-    fn = lib.iqk_gemv_floor_grid if floor == "grid" else lib.iqk_gemv_floor if floor else lib.iqk_gemv
+    fast = _native.launcher()
+    kind = 2 if floor == "grid" else 1 if floor else 0
+    fn = (lib.iqk_gemv, lib.iqk_gemv_floor, lib.iqk_gemv_floor_grid)[kind]
+    ptrs_addr = ctypes.addressof(ptrs)
     # gridDim.y carries the pair index: launch in pair chunks that keep whole
     # activation rows together.
     limit = (65535 // pairs_per_row) * pairs_per_row
     stream = _stream_ptr(device)
+    mid = _native.MEMBER_IDS[member]
+    xp, sp, yp = x.data_ptr(), sel.data_ptr(), out.data_ptr()
     for m0 in range(0, mats, limit):
         cnt = min(limit, mats - m0)
-        rc = fn(_native.MEMBER_IDS[member], n, out_features, num_experts,
-                x.data_ptr() + (m0 // pairs_per_row) * n * 2, ptrs, n_streams,
-                sel.data_ptr() + 4 * m0, pairs_per_row, cnt, out.data_ptr() + m0 * out_features * 2, stream)
+        args = (mid, n, out_features, num_experts, xp + (m0 // pairs_per_row) * n * 2, ptrs_addr, n_streams,
+                sp + 4 * m0, pairs_per_row, cnt, yp + m0 * out_features * 2, stream)
+        rc = fast.gemv(kind, *args) if fast is not None else fn(*args[:5], ptrs, *args[6:])
         if rc:  # the message is formatted only for a failure
             _native.check(rc, f"iqk_gemv{'_floor' if floor else ''}({member}, {n}x{out_features})")
     return out

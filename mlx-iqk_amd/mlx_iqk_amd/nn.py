@@ -102,7 +102,9 @@ class IqkSwitchLinear(torch.nn.Module):
         # dropped whenever a stream is reassigned or the module moves, and
         # re-checked whenever a stream's address differs from the record's
         # (register_buffer and ``.data =`` bypass __setattr__)
-        object.__setattr__(self, "_stream_set", frozenset(self.stream_names()))
+        names = tuple(component_shapes(member, num_experts, out_features, in_features))
+        object.__setattr__(self, "_stream_names", names)
+        object.__setattr__(self, "_stream_set", frozenset(names))
         object.__setattr__(self, "_checked_streams", None)
         object.__setattr__(self, "_checked_sig", None)
 
@@ -121,7 +123,7 @@ class IqkSwitchLinear(torch.nn.Module):
         tensor; one of another shape or dtype on the same address can only
         be a view of the same storage, which stays allocated)."""
         streams = self._streams()
-        sig = tuple(t.data_ptr() for t in streams)
+        sig = [t.data_ptr() for t in streams]
         if self._checked_streams is None or sig != self._checked_sig:
             object.__setattr__(self, "_checked_streams", kernels.CheckedStreams(
                 self.member, streams, self.num_experts, self.out_features, self.in_features))
@@ -132,10 +134,11 @@ class IqkSwitchLinear(torch.nn.Module):
 
     def stream_names(self) -> list[str]:
         """The member's stream buffer names, ordered as the kernels take them."""
-        return list(component_shapes(self.member, self.num_experts, self.out_features, self.in_features))
+        return list(self._stream_names)
 
     def _streams(self) -> list[torch.Tensor]:
-        return [getattr(self, name) for name in self.stream_names()]
+        buffers = self._buffers  # the stream buffers, without Module.__getattr__'s lookups
+        return [buffers[name] for name in self._stream_names]
 
     def load_streams(self, streams: dict) -> None:
         """Install packed streams (numpy arrays or tensors), checking every shape.
@@ -220,9 +223,11 @@ class IqkSwitchLinear(torch.nn.Module):
     def gemv(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         """Fused GEMV over the selected experts; valid for any pair count
         (reference: src/mlx_iqk/nn.py:240-271)."""
-        xt = x.reshape(-1, self.in_features).to(torch.float16).contiguous()
+        xt = x.reshape(-1, self.in_features)
+        if xt.dtype != torch.float16 or not xt.is_contiguous():
+            xt = xt.to(torch.float16).contiguous()
         sel = self._device_ids(indices)
-        mats, rows = int(sel.numel()), int(xt.shape[0])
+        mats, rows = sel.numel(), xt.shape[0]
         # Pairs sharing one activation row: top_k for gate/up, 1 for down.
         if rows <= 0 or mats % rows:
             raise IqkRuntimeError(
@@ -230,7 +235,7 @@ class IqkSwitchLinear(torch.nn.Module):
                 "the operand and the routing disagree")
         out = kernels.gemv(self.member, xt, self._checked(), sel, mats // rows, self.num_experts,
                            self.out_features)
-        return out.reshape(list(indices.shape) + [self.out_features]).unsqueeze(-2)
+        return out.view(*indices.shape, 1, self.out_features)
 
     def gemv_sorted(self, x: torch.Tensor, sorted_ids: torch.Tensor, toks: torch.Tensor) -> torch.Tensor:
         """Fused GEMV over expert-sorted pairs, one workgroup per pair
@@ -262,6 +267,8 @@ class IqkSwitchLinear(torch.nn.Module):
         clamped to [-1, num_experts] first, so no out-of-range id wraps into
         the stack."""
         flat = indices.reshape(-1)
+        if flat.dtype == torch.int32 and flat.is_contiguous():
+            return flat
         if flat.dtype not in (torch.int32, torch.uint32):
             flat = torch.clamp(flat.to(torch.int64), -1, self.num_experts)
         return flat.to(torch.int32).contiguous()

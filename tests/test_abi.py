@@ -180,3 +180,20 @@ def test_pack_refuses_bad_arguments(lib):
     assert f(0, 2048, 8, ctypes.c_void_p(18), streams, 5, None) == _native.ERR_ARGUMENT  # wire alignment
     assert f(0, 2048, 8, p, _native.pointer_array([24] + [16] * 4), 5, None) == _native.ERR_ARGUMENT  # qs alignment
     assert f(0, 2048, 0, p, streams, 5, None) == _native.OK
+
+
+def test_launch_binding_is_built_from_the_same_sources_and_refuses_as_the_abi(lib):
+    """The CPython binding of the decode launch path calls the same entry
+    points (refusals come back unchanged, before any launch)."""
+    fast = _native.launcher()
+    assert fast is not None, "the launch binding is built beside the library by build()"
+    assert fast.source_hash() == lib.iqk_hip_source_hash().decode()
+    streams = _native.pointer_array([16] * 5)
+    addr = ctypes.addressof(streams)
+    assert fast.gemv(0, 7, 4096, 2048, 256, 16, addr, 5, 16, 6, 12, 16, 0) == _native.ERR_MEMBER
+    assert fast.gemv(0, 0, 4096, 2048, 256, 16, addr, 4, 16, 6, 12, 16, 0) == _native.ERR_ARGUMENT  # streams
+    assert fast.gemv(1, 1, 3072, 2048, 256, 16, addr, 4, 16, 6, 12, 16, 0) == _native.ERR_GEOMETRY  # floor
+    assert fast.gemv(2, 0, 4096, 2048, 256, 0, addr, 5, 16, 6, 12, 16, 0) == _native.ERR_ARGUMENT  # null x
+    assert fast.gemv(0, 0, 4096, 2048, 256, 16, addr, 5, 16, 6, 0, 16, 0) == 0  # no pairs: no launch
+    with pytest.raises(TypeError):
+        fast.gemv(0, 0, 4096)
