@@ -119,12 +119,12 @@ int iqk_gemv_sorted(int member, int64_t in_features, int64_t out_features, int64
 // The same contraction, each run of equal adjacent ids decoded together
 // (replaces gemv_union_kernel + IqkSwitchLinear.gemv_union,
 // src/mlx_iqk/kernels.py:484-578, 834-853, src/mlx_iqk/nn.py:301-333).
-// Arguments, output and refusals as iqk_gemv_sorted.  A workgroup serves up
-// to three adjacent pairs of one expert id (a run is cut at multiples of
-// three): it loads and expands the expert's rows once and runs each pair's
-// MFMAs and folds on them, so every output element is iqk_gemv's, bit for
-// bit.  (The reference computes a whole run in one threadgroup; here longer
-// segments cost occupancy: four or five pairs a workgroup measured slower.)
+// Arguments, output and refusals as iqk_gemv_sorted.  A workgroup serves
+// three adjacent pairs (pairs 3z .. 3z+2): for each run of equal ids among
+// them it loads and expands the expert's rows once and runs each pair's MFMAs
+// and folds on them, so every output element is iqk_gemv's, bit for bit.
+// (The reference computes a whole run in one threadgroup; here a run is cut
+// at multiples of three: more staged pairs a workgroup cost occupancy.)
 int iqk_gemv_union(int member, int64_t in_features, int64_t out_features, int64_t num_experts,
                    const void *x, int64_t n_x_rows, const void *const *streams, int n_streams,
                    const uint32_t *sorted_ids, const uint32_t *toks, uint32_t mats,

@@ -855,8 +855,8 @@ enum GemvKind : int { kDecode = 0, kFloor = 1, kFloorGrid = 2 };
 // How a launch maps pairs to activation rows and stream reads.
 // Either way one workgroup serves one (row tile, pair).  Pairs sorted by
 // expert put a run's workgroups next to each other in the grid, so the run's
-// expert rows come from HBM once and from L2 for the run's other pairs: the
-// union form (the reference's one read per run) is this dispatch.
+// later reads of its expert's rows mostly hit L2; the union form
+// (gemv_mfma_union_kernel) decodes a run's pairs together instead.
 enum GemvMode : int {
     kPairs = 0,   // pair m reads x[m / pairs_per_row]
     kSorted = 1,  // pair m reads x[toks[m]]
@@ -1135,14 +1135,13 @@ void gemv_mfma_pairs_kernel(Gemv2Args a) {
 
 // The union form (sorted pairs, IQ2 members; reference: the first pair of a
 // run of equal ids computes the run, src/mlx_iqk/kernels.py:484-572): a
-// workgroup serves a segment of up to PM adjacent pairs with one expert id.
-// Pair m starts a segment when m % PM == 0 or its id differs from pair
-// m - 1's; the segment runs on while the id repeats, up to the next multiple
-// of PM (so a workgroup decides from at most PM + 1 ids).  The segment's
-// expert rows are loaded and expanded once for all its pairs; each pair
-// stages its own activation row (a run's pairs are different tokens); the
-// workgroups of a segment's later pairs exit at once.  Every pair's output is
-// the pair GEMV's, bit for bit.
+// workgroup serves PM adjacent pairs, m0 = PM z .. m0 + PM - 1, and within
+// them each run of equal ids together.  It stages every pair's activation row
+// (a run's pairs are different tokens), then for each run loads the expert's
+// rows once and expands its B operands once for all the run's pairs; the
+// runs of a chunk follow one another, a run's loads issued once the previous
+// run's decode is done with its registers.  Every pair's output is the pair
+// GEMV's, bit for bit.
 template <int MEMBER, int N, int PM>
 struct GemvUnionSmem {
     uint8_t dig[PM][3 * kPlaneStride<N>] __attribute__((aligned(16)));
@@ -1167,90 +1166,92 @@ void gemv_mfma_union_kernel(Gemv2Args a) {
     const int wave = tid >> 6, l = tid & 63;
     const int n = l & 15, g = l >> 4;
     const int kq = wave % KS, tile = wave / KS;
-    const uint32_t m0 = blockIdx.z;
+    const uint32_t m0 = blockIdx.z * PM;
     const uint32_t rowg = blockIdx.x * ROWS;
+    const int cnt = a.mats - m0 < uint32_t(PM) ? int(a.mats - m0) : PM;  // uniform, >= 1
 
-    // The segment (uniform): a later pair of a segment exits; a head counts
-    // the pairs after it with its id, up to the next multiple of PM.
-    const uint32_t e_raw = a.sel[m0];
-    if (m0 % PM != 0 && a.sel[m0 - 1] == e_raw) return;
-    int np = 1;
+    uint32_t id[PM], tok[PM];
 #pragma unroll
-    for (int p = 1; p < PM; ++p)
-        if (np == p && m0 + p < a.mats && (m0 + p) % PM != 0 && a.sel[m0 + p] == e_raw) np = p + 1;
-    uint32_t tok[PM];
-#pragma unroll
-    for (int p = 0; p < PM; ++p) tok[p] = p < np ? a.toks[m0 + uint32_t(p)] : 0u;
-    // an id beyond the stack reads expert 0 (in bounds) and writes NaN rows; a
-    // row beyond x reads row 0 and writes NaN
-    const bool valid = e_raw < a.num_experts;
-    const uint32_t e = valid ? e_raw : 0u;
-
-    // activation loads first (they do not wait for the expert's rows)
+    for (int p = 0; p < PM; ++p) {
+        id[p] = p < cnt ? a.sel[m0 + uint32_t(p)] : 0xffffffffu;
+        tok[p] = p < cnt ? a.toks[m0 + uint32_t(p)] : 0u;
+    }
     const bool stager = tid < S::UNITS;  // uniform per wavefront
     uint4_t xv[PM];
 #pragma unroll
     for (int p = 0; p < PM; ++p) {
         xv[p] = uint4_t{0u, 0u, 0u, 0u};
-        if (p < np && stager)
+        if (p < cnt && stager)
             xv[p] = load_u4(bytes(a.x) + ((tok[p] < a.n_x_rows ? tok[p] : 0u) * (2 * N) + 16 * uint32_t(tid)));
     }
     constexpr bool KTAB = MEMBER == IQ2_K;
     uint2_t ktv = {0u, 0u};
     if (KTAB && tid < 32) ktv = reinterpret_cast<const uint2_t *>(kIq2kTab.w)[tid];
-    LaneOf<MEMBER, N> lane;  // rows rowg + 16 tile + n of the segment's expert
-    lane.load(a, e * a.out_features + rowg + 16 * tile + n, kq, g);
+    const auto expert = [&](int p) { return id[p] < a.num_experts ? id[p] : 0u; };
+    LaneOf<MEMBER, N> lane;
+    lane.load(a, expert(0) * a.out_features + rowg + 16 * tile + n, kq, g);
 
     if (KTAB && tid < 32) sm.ktab[tid] = ktv;
     if (tid < kZeroSpan<MEMBER, N> / 16) reinterpret_cast<uint4_t *>(sm.zero)[tid] = uint4_t{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int p = 0; p < PM; ++p)
-        if (p < np && stager)
+        if (p < cnt && stager)
             stage_activations<N, true, 0, kExpBlock<MEMBER>>(sm.dig[p], sm.sbs[p],
                                                              MEMBER == IQ2_KS ? sm.aux[p] : nullptr, nullptr,
                                                              MEMBER == IQ2_K ? sm.aux[p] : nullptr, tid, xv[p]);
     __syncthreads();
-    const int ai = l & 15;  // this lane's A row
+    const int ai = l & 15;
     const bool data = (ai >> 2) == g && (ai & 3) < 3;
-    const uint8_t *abase[PM];
-    const float *sbs[PM], *aux[PM];
 #pragma unroll
-    for (int p = 0; p < PM; ++p) {
-        abase[p] = data ? sm.dig[p] + (ai & 3) * kPlaneStride<N> + S::WK * kq + 64 * g : sm.zero;
-        sbs[p] = sm.sbs[p] + (S::WK / kExpBlock<MEMBER>) * kq;
-        aux[p] = sm.aux[p] + (S::WK / (MEMBER == IQ2_KS ? 32 : 16)) * kq;
+    for (int st = 0; st < PM; ++st) {
+        if (st < cnt && (st == 0 || id[st] != id[st - 1])) {
+            int np = 1;
+#pragma unroll
+            for (int p = 1; p < PM - st; ++p)
+                if (np == p && st + p < cnt && id[st + p] == id[st]) np = p + 1;
+            if (st > 0) lane.load(a, expert(st) * a.out_features + rowg + 16 * tile + n, kq, g);
+            const uint8_t *abase[PM];
+            const float *sbs[PM], *aux[PM];
+#pragma unroll
+            for (int p = 0; p < PM; ++p) {
+                const int q = st + p < PM ? st + p : PM - 1;
+                abase[p] = data ? sm.dig[q] + (ai & 3) * kPlaneStride<N> + S::WK * kq + 64 * g : sm.zero;
+                sbs[p] = sm.sbs[q] + (S::WK / kExpBlock<MEMBER>) * kq;
+                aux[p] = sm.aux[q] + (S::WK / (MEMBER == IQ2_KS ? 32 : 16)) * kq;
+            }
+            float acc[PM];
+            if constexpr (MEMBER == IQ2_KS)
+                lane.template decode_pairs<PM>(abase, sbs, aux, np, g, acc);
+            else
+                lane.template decode_pairs<PM>(abase, sbs, aux, sm.ktab, np, g, acc);
+#pragma unroll
+            for (int p = 0; p < PM - st; ++p)
+                if (p < np) sm.part[st + p][kq][g][16 * tile + n] = acc[p];
+        }
     }
-    float acc[PM];
-    if constexpr (MEMBER == IQ2_KS)
-        lane.template decode_pairs<PM>(abase, sbs, aux, np, g, acc);
-    else
-        lane.template decode_pairs<PM>(abase, sbs, aux, sm.ktab, np, g, acc);
-#pragma unroll
-    for (int p = 0; p < PM; ++p)
-        if (p < np) sm.part[p][kq][g][16 * tile + n] = acc[p];
     __syncthreads();
-    if (tid < ROWS * np) {
+    if (tid < ROWS * cnt) {
         const int p = tid / ROWS, row = tid % ROWS;
         float sum = 0.f;
 #pragma unroll
         for (int k = 0; k < KS; ++k)
             sum += (sm.part[p][k][0][row] + sm.part[p][k][1][row]) + (sm.part[p][k][2][row] + sm.part[p][k][3][row]);
-        bool x_ok = false;
+        bool ok = false;
 #pragma unroll
         for (int q = 0; q < PM; ++q)
-            if (q == p) x_ok = tok[q] < a.n_x_rows;
+            if (q == p) ok = id[q] < a.num_experts && tok[q] < a.n_x_rows;
         a.y[size_t(m0 + uint32_t(p)) * a.out_features + rowg + uint32_t(row)] =
-            valid && x_ok ? uint16_t(float_to_half_bits(sum)) : kHalfNaN;
+            ok ? uint16_t(float_to_half_bits(sum)) : kHalfNaN;
     }
 }
 
-// Pairs a union workgroup serves at most.  A pair's staged activations take
-// 12.3 KB of LDS (4096 wide), so three pairs keep three workgroups a CU.
+// Pairs a union workgroup serves.  A pair's staged activations take 12.3 KB
+// of LDS (4096 wide), so three pairs keep three workgroups a CU.
 constexpr int kUnionPairs = 3;
 
 template <int MEMBER>
 int launch_union(int64_t n, const Gemv2Args &a, uint32_t mats, hipStream_t st) {
-    const dim3 grid{a.out_features / kGroupRows, 1u, mats};
+    const dim3 grid{a.out_features / kGroupRows, 1u, (mats + kUnionPairs - 1) / kUnionPairs};
     if (n == 4096)
         hipLaunchKernelGGL((gemv_mfma_union_kernel<MEMBER, 4096, kUnionPairs>), grid,
                            dim3{uint32_t(Gemv2Shape<MEMBER, 4096>::THREADS)}, 0, st, a);

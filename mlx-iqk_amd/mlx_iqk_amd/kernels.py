@@ -268,9 +268,9 @@ def gemv_sorted(member: str, x: torch.Tensor, streams: list[torch.Tensor], sorte
     (expert, activation row), bit for bit.  ``union=True`` is the union entry
     point (the multi-token verify shape, src/mlx_iqk/kernels.py:484-578),
     otherwise the sorted one (src/mlx_iqk/kernels.py:404-482).  The sorted
-    form runs one workgroup per pair; the union form gives up to three
-    adjacent pairs of one expert a workgroup, which loads and expands the
-    expert's rows once for them.  IQ2 members only.
+    form runs one workgroup per pair; the union form gives three adjacent
+    pairs a workgroup, which loads and expands the rows of each run of one
+    expert among them once.  IQ2 members only.
     """
     check_iq2_member(member)
     n = int(x.shape[-1])

@@ -254,9 +254,9 @@ class IqkSwitchLinear(torch.nn.Module):
         """:meth:`gemv_sorted` decoding each run of equal adjacent ids
         together: the multi-token verify shape, where several pairs select one
         expert (reference: src/mlx_iqk/nn.py:301-333).  Output identical to
-        :meth:`gemv_sorted` bit for bit; up to three adjacent pairs of one
-        expert share a workgroup, which loads and expands the expert's rows
-        once for them.  The caller applies the inverse permutation."""
+        :meth:`gemv_sorted` bit for bit; three adjacent pairs share a
+        workgroup, which loads and expands the rows of each run of one expert
+        among them once.  The caller applies the inverse permutation."""
         xt, sel, tok = self._sorted_operands(x, sorted_ids, toks)
         return kernels.gemv_sorted(self.member, xt, self._checked(), sel, tok, self.num_experts,
                                    self.out_features, union=True)

@@ -390,6 +390,34 @@ def test_union_runs_past_the_id_batch_and_invalid_ids(device, member):
 
 
 @pytest.mark.parametrize("member", IQ2)
+@pytest.mark.parametrize("tail", (0, 1, 2))
+def test_union_serves_every_run_layout_of_a_workgroup(device, member, tail):
+    """A union workgroup serves pairs 3z .. 3z+2: one run of three, runs of
+    two and one in either order, three runs, an id repeated after another
+    (unsorted input), invalid ids inside and at the edge of a group, and a
+    last group of 1 or 2 pairs.  Equal to the sorted form bit for bit, NaN
+    rows exactly for the invalid ids; also for 1 and 2 pairs in all."""
+    n = 2048
+    module, _ = _module(member, n, 103, device)
+    groups = [(5, 5, 5), (5, 5, 6), (6, 7, 7), (1, 2, 3), (2, 4, 2), (EXPERTS, 0, 0), (0, 0xFFFFFFFF, 1),
+              (3, 3, EXPERTS)]
+    ids = np.array([e for grp in groups for e in grp] + [4, 4][:tail], dtype=np.uint32)
+    rng = np.random.default_rng(107 + tail)
+    rows = 7
+    x = torch.from_numpy(rng.standard_normal((rows, n)).astype(np.float16)).to(device)
+    for k in (ids.size, 1, 2):
+        print(f"union run layouts {member} pairs={k}", flush=True)
+        sel = torch.from_numpy(ids[:k].view(np.int32)).to(device)
+        toks = torch.from_numpy(rng.integers(0, rows, size=k).astype(np.int32)).to(device)
+        ys, yu = (kernels.gemv_sorted(member, x, module._streams(), sel, toks, EXPERTS, OUT, union=u)
+                  for u in (False, True))
+        assert np.array_equal(_bits(yu), _bits(ys))
+        bad = ids[:k] >= EXPERTS
+        y = yu.float().cpu().numpy()
+        assert np.all(np.isnan(y[bad])) and not np.any(np.isnan(y[~bad]))
+
+
+@pytest.mark.parametrize("member", IQ2)
 @pytest.mark.parametrize("n", (2048, 4096))
 @pytest.mark.parametrize("out", (OUT, 48))
 def test_sorted_gemv_is_bit_identical_to_the_pair_gemv(device, member, n, out):
