@@ -11,7 +11,9 @@ those workloads launch runs here against the oracle:
 * IQ1_S_R4 routed decode, 1 token x top-6 (and 2 and 4 tokens, the two-row-
   block form) at both geometries;
 * the 2048-token Zipf(1.1) mixed-member prefill (IQ2_KS gate, IQ2_K down),
-  sorted, through the fused route and the producer + grouped GEMM route.
+  sorted, through the fused route and the producer + grouped GEMM route, and
+  its gate projection in IQ1_S_R4 and in IQ2_K;
+* the decode workloads and the prefill again on codec-quantized stacks.
 
 Stacks are serving-scale random ik wire (every code, scale index and
 alphabet/shift value occurs), relaid on the GPU by ``load_wire``; the
@@ -238,35 +240,38 @@ def test_decode_is_deterministic(device, which):
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
-def test_zipf_prefill_2048_tokens_mixed_members(device):
+def _zipf_prefill(device, projections, quantized=False, seed=505):
     """2048 tokens, Zipf(1.1) top-6 over 256 experts, pairs sorted by expert
-    (sorted_indices=True, 12,288 pairs): gate in IQ2_KS [2048 x 4096], down in
-    IQ2_K [4096 x 2048] on an N(0, 1) fp16 intermediate.  Both routes (fused;
-    producer + grouped GEMM) meet the prefill gate on sampled pairs spanning
-    the largest and the smallest experts, agree with each other over the whole
-    output, and repeat bit for bit."""
+    (sorted_indices=True, 12,288 pairs), for each (name, member, (out, n)):
+    both routes (fused; producer + grouped GEMM) meet the prefill gate on
+    sampled pairs spanning the largest and the smallest experts, agree with
+    each other over the whole output, and repeat bit for bit."""
     tokens = 2048
-    idx = synth.zipf_routing(tokens, E, TOP_K, 1.1, seed=505)
+    idx = synth.zipf_routing(tokens, E, TOP_K, 1.1, seed=seed)
     flat = idx.reshape(-1)
     order = np.argsort(flat, kind="stable")
     ids = flat[order].astype(np.int32)  # the sorting caller's pair order
     counts = np.bincount(ids, minlength=E)
     assert counts.max() > 500 and (counts > 0).sum() > 200, counts
-    rng = np.random.default_rng(506)
+    rng = np.random.default_rng(seed + 1)
     xtok = rng.standard_normal((tokens, GU[1])).astype(np.float16)
     # x [P, 1, in] with indices [P]: the operands of a sorting caller
-    # (mlx_lm's _gather_sort, which the reference's switch layer runs under)
-    inputs = {"gate": xtok[order // TOP_K].reshape(-1, 1, GU[1]),
-              "down": rng.standard_normal((ids.size, 1, DN[1])).astype(np.float16)}
+    # (mlx_lm's _gather_sort, which the reference's switch layer runs under);
+    # the down projection's input is an N(0, 1) fp16 intermediate
+    inputs = {GU[1]: xtok[order // TOP_K].reshape(-1, 1, GU[1]),
+              DN[1]: rng.standard_normal((ids.size, 1, DN[1])).astype(np.float16)}
     # sampled pairs: both ends of the sorted order, the largest expert's run, and random ones
     big = int(np.argmax(counts))
     start = int(np.searchsorted(ids, big))
     picks = np.unique(np.concatenate([[0, 1, ids.size - 1], start + np.arange(4), rng.choice(ids.size, 24, replace=False)]))
     it = torch.from_numpy(ids).to(device)
-    for name, member, (out, n) in (("gate", "iq2_ks", GU), ("down", "iq2_k", DN)):
-        module, wire = _stack(member, out, n, wirepack.seed_for("config", member, name), device)
-        xt = torch.from_numpy(inputs[name]).to(device)
-        print(f"  prefill {name} ({member}) fused", flush=True)
+    for name, member, (out, n) in projections:
+        if quantized:
+            module, wire = _quantized_stack(member, out, n, wirepack.seed_for("quantized", member, name), device)
+        else:
+            module, wire = _stack(member, out, n, wirepack.seed_for("config", member, name), device)
+        xt = torch.from_numpy(inputs[n]).to(device)
+        print(f"  prefill {name} ({member}{', quantized' if quantized else ''}) fused", flush=True)
         module.fused_prefill = True
         fused = module(xt, it, sorted_indices=True)
         again = module(xt, it, sorted_indices=True)
@@ -283,7 +288,29 @@ def test_zipf_prefill_2048_tokens_mixed_members(device):
         f, p = f.cpu().numpy(), p.cpu().numpy()
         rows = _rows_sample(rng, out, 64, member)
         for q in picks:
-            want = _expected(member, wire, out, n, int(ids[q]), rows, inputs[name][q, 0])
+            want = _expected(member, wire, out, n, int(ids[q]), rows, inputs[n][q, 0])
             for got, route in ((f, "fused"), (p, "producer")):
                 rel = np.max(np.abs(got[q, rows] - want)) / np.max(np.abs(want))
-                assert rel < 3e-3, (name, route, int(q), rel)
+                assert rel < 3e-3, (name, member, route, int(q), rel)
+        del fused, again, producer
+        torch.cuda.empty_cache()
+
+
+def test_zipf_prefill_2048_tokens_mixed_members(device):
+    """The prefill workload: gate in IQ2_KS [2048 x 4096], down in IQ2_K
+    [4096 x 2048], serving-scale random wire."""
+    _zipf_prefill(device, (("gate", "iq2_ks", GU), ("down", "iq2_k", DN)))
+
+
+def test_zipf_prefill_on_codec_quantized_stacks(device):
+    """The same prefill on stacks of N(0, 0.02) rows quantized by the package
+    codec (the workloads' data), both routes against the oracle."""
+    _zipf_prefill(device, (("gate", "iq2_ks", GU), ("down", "iq2_k", DN)), quantized=True, seed=515)
+
+
+@pytest.mark.parametrize("member", ("iq1_s_r4", "iq2_k"))
+def test_zipf_prefill_gate_in_the_other_members(device, member):
+    """The gate projection of the prefill in IQ1_S_R4 and in IQ2_K (the
+    fused kernel's other instantiations at 4096 wide), both routes against
+    the oracle."""
+    _zipf_prefill(device, (("gate", member, GU),), seed=525)
