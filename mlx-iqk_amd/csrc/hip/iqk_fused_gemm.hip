@@ -68,6 +68,7 @@ constexpr int kXChunks = 2 * kFusedKS / 16;      // 16-byte chunks of a staged r
 constexpr int kXRows = kFusedThreads / kXChunks; // rows one staging pass covers
 constexpr int kXPer = kFusedBM / kXRows;         // staging passes a step
 static_assert(kFusedBM % kXRows == 0 && kFusedThreads >= 256, "whole staging passes; the work-list scan needs 256 threads");
+static_assert(kXRows == 32, "staging pass i is the 32-row MFMA slot block i");
 
 struct FusedArgs {
     const uint16_t *x;
@@ -359,9 +360,11 @@ void fused_gemm_kernel(FusedArgs a) {
             slot_dst[row] = dst;
         }
     }
-    const auto load_x = [&](int s, uint4_t *v) {
+    // Staging pass i covers slot block i (rows 32i .. 32i+31): a tile of
+    // MB slot blocks loads and stages passes 0 .. MB-1 only.
+    const auto load_x = [&](int s, uint4_t *v, auto passes) {
 #pragma unroll
-        for (int i = 0; i < kXPer; ++i)
+        for (int i = 0; i < decltype(passes)::value; ++i)
             if (xlive[i]) v[i] = load_u4(xbase + xoff[i] + uint32_t(2 * kFusedKS * s));
     };
     // Each 8-element chunk is stored in the order (0,4,1,5,2,6,3,7), the
@@ -386,10 +389,10 @@ void fused_gemm_kernel(FusedArgs a) {
                     uint4_t{0u, 0u, 0u, 0u};
         }
     }
-    const auto store_x = [&](int buf, const uint4_t *v) {
+    const auto store_x = [&](int buf, const uint4_t *v, auto passes) {
         uint8_t *dst = xs[buf] + xrow_l * kXStride + 16 * xchunk;
 #pragma unroll
-        for (int i = 0; i < kXPer; ++i)
+        for (int i = 0; i < decltype(passes)::value; ++i)
             if (xlive[i])
                 *reinterpret_cast<uint4_t *>(dst + kXRows * kXStride * i) =
                     uint4_t{perm(v[i].z, v[i].x, xsel_lo[i]), perm(v[i].z, v[i].x, xsel_hi[i]),
@@ -420,14 +423,15 @@ void fused_gemm_kernel(FusedArgs a) {
     };
 
     uint4_t xa[kXPer];
-    load_x(0, xa);
+    constexpr std::integral_constant<int, kXPer> kAllPasses{};
+    load_x(0, xa, kAllPasses);
     // IQ2_K without a dv plane in LDS: this lane's dv words, one per four steps
     const uint32_t *dvp = reinterpret_cast<const uint32_t *>(static_cast<const uint8_t *>(a.s3) + row0 * (K / 128) +
                                                              wl * uint32_t(K / 128));
     constexpr bool DV_WORDS = MEMBER == IQ2_K && !S::DV_IN_LDS;
     uint32_t dvw = DV_WORDS ? dvp[0] : 0u, dvn = 0u;
     uint4_t q = load_q(0), qn;
-    store_x(0, xa);
+    store_x(0, xa, kAllPasses);
     __syncthreads();  // scale planes and the first activations are in LDS
     // row scale: IQ2_KS from LDS (rows past out_features read LDS junk, never
     // stored), IQ1_S_R4 from its stream (an in-bounds row); IQ2_K's are per
@@ -452,7 +456,7 @@ void fused_gemm_kernel(FusedArgs a) {
         for (int s = 0; s < STEPS; ++s) {
             const bool more = s + 1 < STEPS;
             if (more) {
-                load_x(s + 1, xa);
+                load_x(s + 1, xa, slot_blocks);
                 qn = load_q(s + 1);
             }
             if constexpr (DV_WORDS) {
@@ -497,7 +501,7 @@ void fused_gemm_kernel(FusedArgs a) {
                 }
             }
             if (more) {
-                store_x((s + 1) & 1, xa);  // the buffer every wavefront finished reading before the last barrier
+                store_x((s + 1) & 1, xa, slot_blocks);  // the buffer every wavefront finished reading before the last barrier
                 q = qn;
             }
             if constexpr (DV_WORDS) {
