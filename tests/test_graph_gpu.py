@@ -81,3 +81,49 @@ def test_forward_replays_from_a_graph(device, member, route):
         assert out.shape == want.shape
         assert bool(torch.isfinite(want).all())
         assert torch.equal(out, want), f"replay {replay} differs from eager execution"
+
+
+@pytest.mark.parametrize("member", ("iq2_ks", "iq2_k"))
+@pytest.mark.parametrize("method", ("gemv_sorted", "gemv_union"))
+def test_sorted_and_union_replay_from_a_graph(device, member, method):
+    """The verify shapes' entry points inside a graph: 8 tokens, each routed
+    to the same 3 of the experts in its own order (three runs of 8 pairs, so
+    groups of three pairs hold one or two runs), a new pool and new
+    activations written in place before each replay."""
+    module = _module(member, 43, device)
+    tokens, top_k = 8, 3
+    rng = np.random.default_rng(7)
+    x = torch.empty(tokens, 1, 1, N, dtype=torch.float16, device=device)
+    ids = torch.empty(tokens * top_k, dtype=torch.int32, device=device)
+    toks = torch.empty(tokens * top_k, dtype=torch.int32, device=device)
+
+    def fill():
+        x.copy_(torch.from_numpy(rng.standard_normal((tokens, 1, 1, N)).astype(np.float16)))
+        pool = rng.choice(EXPERTS, 3, replace=False)
+        idx = np.stack([rng.permutation(pool)[:top_k] for _ in range(tokens)]).reshape(-1)
+        order = np.argsort(idx, kind="stable")
+        ids.copy_(torch.from_numpy(idx[order].astype(np.int32)))
+        toks.copy_(torch.from_numpy((order // top_k).astype(np.int32)))
+
+    def run():
+        return getattr(module, method)(x, ids, toks)
+
+    fill()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            run()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = run()
+    for replay in range(4):
+        fill()
+        want = run()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert bool(torch.isfinite(want).all())
+        assert torch.equal(out, want), f"replay {replay} differs from eager execution"
