@@ -143,6 +143,14 @@ __device__ __forceinline__ uint32_t half_row_mirror(uint32_t v) {
 
 __device__ __forceinline__ int digits_sum(int4_t d) { return (((d.z << 8) + d.y) << 8) + d.x; }
 
+// The three plane sums of an IQ2_K super-block as a float: d.x + 2^8 d.y is
+// exact in int32 (|d.x|, |d.y| < 2^20), so converting it rounds that value
+// once, as fma(float(d.y), 256, float(d.x)) does; the 2^16 plane is added by
+// an fma (the whole sum can pass 2^31).
+__device__ __forceinline__ float planes_sum(int4_t d) {
+    return fmaf(float(d.z), 65536.f, float(d.x + (d.y << 8)));
+}
+
 // 8 x the low / high 16 bits of v.  Plain code, not inline asm: the
 // compiler must see every instruction that writes a register, because a
 // register whose last writer was an MFMA still in flight (an unused dword of
@@ -571,7 +579,7 @@ struct LaneIq2k {
                 const int sp = s - 1;
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const float sum = fmaf(float(Wp[r].z), 65536.f, fmaf(float(Wp[r].y), 256.f, float(Wp[r].x)));
+                    const float sum = planes_sum(Wp[r]);
                     acc[r] = fmaf(fmaf(2.f, sum, offs[r][sp]), dfac[r][sp], acc[r]);
                     pin(acc[r]);
                 }
@@ -619,7 +627,7 @@ struct LaneIq2k {
             int4_t W = int4_t{0, 0, 0, 0};
 #pragma unroll
             for (int j = 0; j < 4; ++j) W = mfma(read_a_all(abase + 256 * s + 16 * j), B[j], W);
-            const float sum = fmaf(float(W.z), 65536.f, fmaf(float(W.y), 256.f, float(W.x)));
+            const float sum = planes_sum(W);
             acc = fmaf(fmaf(2.f, sum, offs), dfac, acc);
         }
         return acc;
@@ -669,7 +677,7 @@ struct LaneIq2k {
                     int4_t W = int4_t{0, 0, 0, 0};
 #pragma unroll
                     for (int j = 0; j < 4; ++j) W = mfma(read_a_all(abase[p] + 256 * s + 16 * j), B[j], W);
-                    const float sum = fmaf(float(W.z), 65536.f, fmaf(float(W.y), 256.f, float(W.x)));
+                    const float sum = planes_sum(W);
                     acc[p] = fmaf(fmaf(2.f, sum, offs), dfac, acc[p]);
                 }
             }
