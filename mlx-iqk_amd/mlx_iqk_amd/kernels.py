@@ -127,11 +127,12 @@ class CheckedStreams:
     one whenever a stream's address, shape, strides or dtype differ from the
     ones it was made from)."""
 
-    __slots__ = ("key", "device", "ptrs", "ptrs_addr", "count", "gemv_ok")
+    __slots__ = ("key", "device", "device_index", "ptrs", "ptrs_addr", "count", "gemv_ok")
 
     def __init__(self, member: str, streams: list[torch.Tensor], num_experts: int, out_features: int,
                  in_features: int):
         self.device = check_streams(member, streams, num_experts, out_features, in_features)
+        self.device_index = self.device.index if self.device.index is not None else torch.cuda.current_device()
         self.key = (member, int(num_experts), int(out_features), int(in_features))
         self.ptrs = _native.pointer_array([t.data_ptr() for t in streams])
         self.ptrs_addr = ctypes.addressof(self.ptrs)
@@ -187,25 +188,49 @@ def gemv(member: str, x: torch.Tensor, streams: list[torch.Tensor], sel: torch.T
             raise IqkKernelError(f"out must be {(mats, out_features)}, got {tuple(out.shape)}")
     if mats == 0:
         return out
-    lib = _native.load()
-    fast = _native.launcher()
     kind = 2 if floor == "grid" else 1 if floor else 0
-    fn = (lib.iqk_gemv, lib.iqk_gemv_floor, lib.iqk_gemv_floor_grid)[kind]
+    _gemv_launch(kind, member, n, out_features, num_experts, x.data_ptr(), ptrs, n_streams, sel.data_ptr(),
+                 pairs_per_row, mats, out.data_ptr(), _stream_ptr(device))
+    return out
+
+
+def _gemv_launch(kind: int, member: str, n: int, out_features: int, num_experts: int, xp: int, ptrs, n_streams: int,
+                 sp: int, pairs_per_row: int, mats: int, yp: int, stream: int) -> None:
+    """The launches of :func:`gemv` (kind 0 decode, 1 floor, 2 grid floor) on
+    operands already checked: device addresses of x, sel and y, the streams'
+    pointer array.  gridDim.y carries the pair index, so the pairs go in
+    chunks that keep whole activation rows together."""
+    fast = _native.launcher()
+    lib = None if fast is not None else _native.load()
     ptrs_addr = ctypes.addressof(ptrs)
-    # gridDim.y carries the pair index: launch in pair chunks that keep whole
-    # activation rows together.
     limit = (65535 // pairs_per_row) * pairs_per_row
-    stream = _stream_ptr(device)
     mid = _native.MEMBER_IDS[member]
-    xp, sp, yp = x.data_ptr(), sel.data_ptr(), out.data_ptr()
     for m0 in range(0, mats, limit):
         cnt = min(limit, mats - m0)
         args = (mid, n, out_features, num_experts, xp + (m0 // pairs_per_row) * n * 2, ptrs_addr, n_streams,
                 sp + 4 * m0, pairs_per_row, cnt, yp + m0 * out_features * 2, stream)
-        rc = fast.gemv(kind, *args) if fast is not None else fn(*args[:5], ptrs, *args[6:])
+        if fast is not None:
+            rc = fast.gemv(kind, *args)
+        else:
+            fn = (lib.iqk_gemv, lib.iqk_gemv_floor, lib.iqk_gemv_floor_grid)[kind]
+            rc = fn(*args[:5], ptrs, *args[6:])
         if rc:  # the message is formatted only for a failure
-            _native.check(rc, f"iqk_gemv{'_floor' if floor else ''}({member}, {n}x{out_features})")
-    return out
+            _native.check(rc, f"iqk_gemv{'_floor' if kind else ''}({member}, {n}x{out_features})")
+
+
+def gemv_checked(member: str, x: torch.Tensor, streams: "CheckedStreams", sel: torch.Tensor, rows: int, mats: int,
+                 out: torch.Tensor, num_experts: int, out_features: int) -> None:
+    """The decode GEMV into ``out`` for operands the caller has checked: x
+    fp16 and contiguous with ``rows`` rows of the streams' width, sel int32
+    and contiguous with ``mats`` ids, out fp16 with ``mats x out_features``
+    elements, all on the streams' GPU, ``streams.gemv_ok`` and
+    ``mats % rows == 0``.  (The switch module's eager decode path: it skips
+    the reshapes and repeated checks of :func:`gemv`.)"""
+    if mats:
+        _gemv_launch(0, member, streams.key[3], out_features, num_experts, x.data_ptr(), streams.ptrs,
+                     streams.count, sel.data_ptr(), mats // rows, mats, out.data_ptr(),
+                     _raw_stream(streams.device_index) if _raw_stream is not None
+                     else torch.cuda.current_stream(streams.device).cuda_stream)
 
 
 def stream_floor_words(nbytes: int, loads: int = 4, max_waves: int = 0) -> int:

@@ -223,6 +223,20 @@ class IqkSwitchLinear(torch.nn.Module):
     def gemv(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         """Fused GEMV over the selected experts; valid for any pair count
         (reference: src/mlx_iqk/nn.py:240-271)."""
+        chk = self._checked()
+        # Operands already in the kernel's layout (fp16 contiguous x, int32
+        # contiguous ids, on the streams' GPU) launch without a reshape and
+        # with the output allocated in its final shape: the eager decode's
+        # host time is mostly such tensor operations.
+        if (x.dtype == torch.float16 and indices.dtype == torch.int32 and chk.gemv_ok
+                and x.is_contiguous() and indices.is_contiguous() and x.shape[-1] == self.in_features
+                and x.get_device() == chk.device_index and indices.get_device() == chk.device_index):
+            mats, rows = indices.numel(), x.numel() // self.in_features
+            if rows > 0 and mats % rows == 0:
+                out = torch.empty((*indices.shape, 1, self.out_features), dtype=torch.float16, device=chk.device)
+                kernels.gemv_checked(self.member, x, chk, indices, rows, mats, out, self.num_experts,
+                                     self.out_features)
+                return out
         xt = x.reshape(-1, self.in_features)
         if xt.dtype != torch.float16 or not xt.is_contiguous():
             xt = xt.to(torch.float16).contiguous()
@@ -233,8 +247,7 @@ class IqkSwitchLinear(torch.nn.Module):
             raise IqkRuntimeError(
                 f"{mats} token-expert pairs do not tile {rows} activation row(s); "
                 "the operand and the routing disagree")
-        out = kernels.gemv(self.member, xt, self._checked(), sel, mats // rows, self.num_experts,
-                           self.out_features)
+        out = kernels.gemv(self.member, xt, chk, sel, mats // rows, self.num_experts, self.out_features)
         return out.view(*indices.shape, 1, self.out_features)
 
     def gemv_sorted(self, x: torch.Tensor, sorted_ids: torch.Tensor, toks: torch.Tensor) -> torch.Tensor:
