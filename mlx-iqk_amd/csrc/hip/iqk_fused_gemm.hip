@@ -349,7 +349,7 @@ void fused_gemm_kernel(FusedArgs a) {
         const bool xv = xrow < a.n_x_rows;
         // a dead slot reads row 0 (the entry point refuses an empty x); its
         // products feed only its own output row, never stored as a value
-        xoff[i] = (xv ? xrow : 0u) * uint32_t(2 * K) + uint32_t(16 * xchunk);
+        xoff[i] = (xv ? xrow : 0u) * uint32_t(2 * K) + uint32_t(16 * xchunk) + (IQ1 && xchunk >= 8 ? 384u : 0u);
         xlive[i] = !IQ1 || xp < gend;
         if (xchunk == 0) {  // one thread a slot: the epilogue's destination, read once
             uint32_t dst = kNoStore;
@@ -362,10 +362,16 @@ void fused_gemm_kernel(FusedArgs a) {
     }
     // Staging pass i covers slot block i (rows 32i .. 32i+31): a tile of
     // MB slot blocks loads and stages passes 0 .. MB-1 only.
+    // IQ1_S_R4 takes its steps in groups of four (below): step 4p + j stages
+    // the 64 elements from 512p + 64j (lane group 0's) and from
+    // 512p + 256 + 64j (lane group 1's); the IQ2 members stage 128 s .. +127.
+    const auto x_step = [&](int s) {
+        return IQ1 ? uint32_t(1024 * (s >> 2) + 128 * (s & 3)) : uint32_t(2 * kFusedKS * s);
+    };
     const auto load_x = [&](int s, uint4_t *v, auto passes) {
 #pragma unroll
         for (int i = 0; i < decltype(passes)::value; ++i)
-            if (xlive[i]) v[i] = load_u4(xbase + xoff[i] + uint32_t(2 * kFusedKS * s));
+            if (xlive[i]) v[i] = load_u4(xbase + xoff[i] + x_step(s));
     };
     // Each 8-element chunk is stored in the order (0,4,1,5,2,6,3,7), the
     // order expand_word_paired gives the weights.  A row past the tile's last
@@ -403,8 +409,12 @@ void fused_gemm_kernel(FusedArgs a) {
     // the block's first row.  The block's first row of each plane is a
     // uniform base, the lane's offsets from it are 32-bit (the entry point
     // refuses an expert plane of 4 GiB or more).  IQ2 members: the step's
-    // four code words; IQ1_S_R4: the two blocks' index words and their qh
-    // words (blocks 4s + 2kg, +1).
+    // four code words.  IQ1_S_R4: steps in groups of four, lane group kg
+    // taking blocks 16p + 8kg .. +7 in group p (blocks 16p + 8kg + 2j, +1 in
+    // its step j), so a lane loads its 32 bytes of index words and 16 bytes
+    // of qh words once a group: each 128-byte line of the two planes is
+    // loaded two and four times, against eight and sixteen with a load a
+    // step (IQ1_S_R4 fetched 2.13x its unique bytes that way).
     const int wave = tid >> 6, l = tid & 63, ln = l & 31, kg = l >> 5;
     const int lrow = 32 * wave + ln;
     const bool wv = lrow < rows_here;
@@ -412,14 +422,22 @@ void fused_gemm_kernel(FusedArgs a) {
     const uint8_t *qbase = static_cast<const uint8_t *>(a.s0) + row0 * QROW;
     const uint8_t *hbase = static_cast<const uint8_t *>(a.s1) + row0 * (K / 16);
     const uint32_t wl = wv ? uint32_t(lrow) : 0u;
-    const uint32_t qoff = wl * QROW + uint32_t((IQ1 ? 8 : 16) * kg), hoff = wl * uint32_t(K / 16) + uint32_t(4 * kg);
-    const auto load_q = [&](int s) {
-        if constexpr (IQ1) {
-            const uint2_t iw = *reinterpret_cast<const uint2_t *>(qbase + qoff + uint32_t(16 * s));
-            return uint4_t{iw.x, iw.y, *reinterpret_cast<const uint32_t *>(hbase + hoff + uint32_t(8 * s)), 0u};
-        } else {
-            return load_u4(qbase + qoff + uint32_t(32 * s));
-        }
+    const uint32_t qoff = wl * QROW + uint32_t((IQ1 ? 32 : 16) * kg), hoff = wl * uint32_t(K / 16) + uint32_t(16 * kg);
+    const auto load_q = [&](int s) { return load_u4(qbase + qoff + uint32_t(32 * s)); };  // IQ2 members
+    struct Iq1Group {
+        uint4_t qs[2], qh;  // index words of the lane's 8 blocks, their 8 qh halves
+    };
+    const auto load_group = [&](int p) {  // IQ1_S_R4: group p
+        Iq1Group gr;
+        gr.qs[0] = load_u4(qbase + qoff + uint32_t(64 * p));
+        gr.qs[1] = load_u4(qbase + qoff + uint32_t(64 * p + 16));
+        gr.qh = load_u4(hbase + hoff + uint32_t(32 * p));
+        return gr;
+    };
+    // step j of a group: blocks 2j, 2j+1 (index words, qh halves in one word)
+    const auto group_step = [](const Iq1Group &gr, int j) {
+        const uint4_t &w = gr.qs[j >> 1];
+        return uint4_t{(j & 1) ? w.z : w.x, (j & 1) ? w.w : w.y, gr.qh[j], 0u};
     };
 
     uint4_t xa[kXPer];
@@ -430,7 +448,12 @@ void fused_gemm_kernel(FusedArgs a) {
                                                              wl * uint32_t(K / 128));
     constexpr bool DV_WORDS = MEMBER == IQ2_K && !S::DV_IN_LDS;
     uint32_t dvw = DV_WORDS ? dvp[0] : 0u, dvn = 0u;
-    uint4_t q = load_q(0), qn;
+    uint4_t q = {0u, 0u, 0u, 0u}, qn;
+    Iq1Group grp{}, grpn{};
+    if constexpr (IQ1)
+        grp = load_group(0);
+    else
+        q = load_q(0);
     store_x(0, xa, kAllPasses);
     __syncthreads();  // scale planes and the first activations are in LDS
     // row scale: IQ2_KS from LDS (rows past out_features read LDS junk, never
@@ -453,11 +476,18 @@ void fused_gemm_kernel(FusedArgs a) {
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[mb][r] = 0.f;
-        for (int s = 0; s < STEPS; ++s) {
+        constexpr int G = IQ1 ? 4 : 1;  // steps a code-word group
+        for (int s0 = 0; s0 < STEPS; s0 += G) {
+#pragma unroll
+          for (int j = 0; j < G; ++j) {
+            const int s = s0 + j;
             const bool more = s + 1 < STEPS;
             if (more) {
                 load_x(s + 1, xa, slot_blocks);
-                qn = load_q(s + 1);
+                if constexpr (!IQ1) qn = load_q(s + 1);
+            }
+            if constexpr (IQ1) {
+                if (j == 0 && s0 + G < STEPS) grpn = load_group((s0 + G) / G);  // the next group, a group ahead
             }
             if constexpr (DV_WORDS) {
                 if ((s & 3) == 0 && s + 4 < STEPS) dvn = dvp[(s >> 2) + 1];  // the next group's word, a group ahead
@@ -465,7 +495,7 @@ void fused_gemm_kernel(FusedArgs a) {
             Pool p[4];
             uint32_t words[4];
             if constexpr (IQ1) {
-                fused_iq1(q, sc.codes, ptab, d, p, words);
+                fused_iq1(group_step(grp, j), sc.codes, ptab, d, p, words);
             } else {
                 fused_pools<MEMBER, K>(sc, lrow, s, kg, d, dvw, ptab, p);
 #pragma unroll
@@ -502,12 +532,16 @@ void fused_gemm_kernel(FusedArgs a) {
             }
             if (more) {
                 store_x((s + 1) & 1, xa, slot_blocks);  // the buffer every wavefront finished reading before the last barrier
-                q = qn;
+                if constexpr (!IQ1) q = qn;
+            }
+            if constexpr (IQ1) {
+                if (j == G - 1) grp = grpn;
             }
             if constexpr (DV_WORDS) {
                 if ((s & 3) == 3) dvw = dvn;
             }
             __syncthreads();
+          }
         }
 
         // D layout (32x32): lane l, register r holds row 8(r/4) + 4(l/32) +
