@@ -270,6 +270,13 @@ void fused_gemm_kernel(FusedArgs a) {
     constexpr bool IQ1 = MEMBER == IQ1_S_R4;
     using S = FusedScales<IQ1 ? IQ2_KS : MEMBER, K>;
     constexpr int STEPS = K / kFusedKS;
+    // Steps a code-word group: IQ1_S_R4 4, the IQ2 members 1.  Two-step
+    // groups for the IQ2 members measured within 1% (IQ2_K gate 404.4 ->
+    // 402.6 us, IQ2_KS gate 381.9 -> 380.8 us with 32 bytes of spills at 128
+    // VGPRs; IQ2_K at 2048 wide has no room for them): their lines are
+    // loaded four times a step-group of one already.
+    constexpr int G = IQ1 ? 4 : 1;
+    static_assert(STEPS % G == 0, "whole groups of steps");
     __shared__ TileScan ts;
     __shared__ __attribute__((aligned(16))) uint8_t xs[2][kFusedBM * kXStride];
     // per slot of the tile: its output row, bit 31 set when its activations
@@ -349,7 +356,7 @@ void fused_gemm_kernel(FusedArgs a) {
         const bool xv = xrow < a.n_x_rows;
         // a dead slot reads row 0 (the entry point refuses an empty x); its
         // products feed only its own output row, never stored as a value
-        xoff[i] = (xv ? xrow : 0u) * uint32_t(2 * K) + uint32_t(16 * xchunk) + (IQ1 && xchunk >= 8 ? 384u : 0u);
+        xoff[i] = (xv ? xrow : 0u) * uint32_t(2 * K) + uint32_t(16 * xchunk) + (xchunk >= 8 ? 128u * (G - 1) : 0u);
         xlive[i] = !IQ1 || xp < gend;
         if (xchunk == 0) {  // one thread a slot: the epilogue's destination, read once
             uint32_t dst = kNoStore;
@@ -362,12 +369,10 @@ void fused_gemm_kernel(FusedArgs a) {
     }
     // Staging pass i covers slot block i (rows 32i .. 32i+31): a tile of
     // MB slot blocks loads and stages passes 0 .. MB-1 only.
-    // IQ1_S_R4 takes its steps in groups of four (below): step 4p + j stages
-    // the 64 elements from 512p + 64j (lane group 0's) and from
-    // 512p + 256 + 64j (lane group 1's); the IQ2 members stage 128 s .. +127.
-    const auto x_step = [&](int s) {
-        return IQ1 ? uint32_t(1024 * (s >> 2) + 128 * (s & 3)) : uint32_t(2 * kFusedKS * s);
-    };
+    // Steps go in groups of G (below): step Gp + j stages the 64 elements
+    // from 128Gp + 64j (lane group 0's) and from 128Gp + 64G + 64j (lane
+    // group 1's).
+    const auto x_step = [&](int s) { return uint32_t(256 * G * (s / G) + 128 * (s % G)); };
     const auto load_x = [&](int s, uint4_t *v, auto passes) {
 #pragma unroll
         for (int i = 0; i < decltype(passes)::value; ++i)
@@ -408,13 +413,14 @@ void fused_gemm_kernel(FusedArgs a) {
     // this lane's weight row and code words; a row past out_features reads
     // the block's first row.  The block's first row of each plane is a
     // uniform base, the lane's offsets from it are 32-bit (the entry point
-    // refuses an expert plane of 4 GiB or more).  IQ2 members: the step's
-    // four code words.  IQ1_S_R4: steps in groups of four, lane group kg
-    // taking blocks 16p + 8kg .. +7 in group p (blocks 16p + 8kg + 2j, +1 in
-    // its step j), so a lane loads its 32 bytes of index words and 16 bytes
-    // of qh words once a group: each 128-byte line of the two planes is
-    // loaded two and four times, against eight and sixteen with a load a
-    // step (IQ1_S_R4 fetched 2.13x its unique bytes that way).
+    // refuses an expert plane of 4 GiB or more).  The steps go in groups of
+    // G, lane group kg taking elements 128Gp + 64G kg .. +64G-1 of group p
+    // (64j .. 64j+63 of those in its step j), so a lane loads its code bytes
+    // once a group: IQ2 members 16G bytes (four words a step), IQ1_S_R4 (G =
+    // 4) 32 bytes of index words and 16 of qh words.  A 128-byte line of a
+    // code plane is then loaded 4/G times (IQ2; IQ1_S_R4 two and four times
+    // against eight and sixteen with a load a step: 2.13x its unique bytes
+    // fetched, 440.5 -> 411.9 us on the Zipf prefill gate).
     const int wave = tid >> 6, l = tid & 63, ln = l & 31, kg = l >> 5;
     const int lrow = 32 * wave + ln;
     const bool wv = lrow < rows_here;
@@ -422,22 +428,30 @@ void fused_gemm_kernel(FusedArgs a) {
     const uint8_t *qbase = static_cast<const uint8_t *>(a.s0) + row0 * QROW;
     const uint8_t *hbase = static_cast<const uint8_t *>(a.s1) + row0 * (K / 16);
     const uint32_t wl = wv ? uint32_t(lrow) : 0u;
-    const uint32_t qoff = wl * QROW + uint32_t((IQ1 ? 32 : 16) * kg), hoff = wl * uint32_t(K / 16) + uint32_t(16 * kg);
-    const auto load_q = [&](int s) { return load_u4(qbase + qoff + uint32_t(32 * s)); };  // IQ2 members
-    struct Iq1Group {
-        uint4_t qs[2], qh;  // index words of the lane's 8 blocks, their 8 qh halves
+    const uint32_t qoff = wl * QROW + uint32_t((IQ1 ? 8 : 16) * G * kg), hoff = wl * uint32_t(K / 16) + uint32_t(16 * kg);
+    struct CodeGroup {
+        uint4_t w[IQ1 ? 3 : G];  // IQ2: step j's words; IQ1_S_R4: 8 blocks' index words, then their qh halves
     };
-    const auto load_group = [&](int p) {  // IQ1_S_R4: group p
-        Iq1Group gr;
-        gr.qs[0] = load_u4(qbase + qoff + uint32_t(64 * p));
-        gr.qs[1] = load_u4(qbase + qoff + uint32_t(64 * p + 16));
-        gr.qh = load_u4(hbase + hoff + uint32_t(32 * p));
+    const auto load_group = [&](int p) {
+        CodeGroup gr;
+        if constexpr (IQ1) {
+            gr.w[0] = load_u4(qbase + qoff + uint32_t(64 * p));
+            gr.w[1] = load_u4(qbase + qoff + uint32_t(64 * p + 16));
+            gr.w[2] = load_u4(hbase + hoff + uint32_t(32 * p));
+        } else {
+#pragma unroll
+            for (int j = 0; j < G; ++j) gr.w[j] = load_u4(qbase + qoff + uint32_t(32 * G * p + 16 * j));
+        }
         return gr;
     };
-    // step j of a group: blocks 2j, 2j+1 (index words, qh halves in one word)
-    const auto group_step = [](const Iq1Group &gr, int j) {
-        const uint4_t &w = gr.qs[j >> 1];
-        return uint4_t{(j & 1) ? w.z : w.x, (j & 1) ? w.w : w.y, gr.qh[j], 0u};
+    // step j of a group; IQ1_S_R4: blocks 2j, 2j+1 (index words, qh halves in one word)
+    const auto group_step = [](const CodeGroup &gr, int j) {
+        if constexpr (IQ1) {
+            const uint4_t &w = gr.w[j >> 1];
+            return uint4_t{(j & 1) ? w.z : w.x, (j & 1) ? w.w : w.y, gr.w[2][j], 0u};
+        } else {
+            return gr.w[j];
+        }
     };
 
     uint4_t xa[kXPer];
@@ -448,12 +462,7 @@ void fused_gemm_kernel(FusedArgs a) {
                                                              wl * uint32_t(K / 128));
     constexpr bool DV_WORDS = MEMBER == IQ2_K && !S::DV_IN_LDS;
     uint32_t dvw = DV_WORDS ? dvp[0] : 0u, dvn = 0u;
-    uint4_t q = {0u, 0u, 0u, 0u}, qn;
-    Iq1Group grp{}, grpn{};
-    if constexpr (IQ1)
-        grp = load_group(0);
-    else
-        q = load_q(0);
+    CodeGroup grp = load_group(0), grpn{};
     store_x(0, xa, kAllPasses);
     __syncthreads();  // scale planes and the first activations are in LDS
     // row scale: IQ2_KS from LDS (rows past out_features read LDS junk, never
@@ -476,19 +485,13 @@ void fused_gemm_kernel(FusedArgs a) {
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[mb][r] = 0.f;
-        constexpr int G = IQ1 ? 4 : 1;  // steps a code-word group
         for (int s0 = 0; s0 < STEPS; s0 += G) {
 #pragma unroll
           for (int j = 0; j < G; ++j) {
             const int s = s0 + j;
             const bool more = s + 1 < STEPS;
-            if (more) {
-                load_x(s + 1, xa, slot_blocks);
-                if constexpr (!IQ1) qn = load_q(s + 1);
-            }
-            if constexpr (IQ1) {
-                if (j == 0 && s0 + G < STEPS) grpn = load_group((s0 + G) / G);  // the next group, a group ahead
-            }
+            if (more) load_x(s + 1, xa, slot_blocks);
+            if (j == 0 && s0 + G < STEPS) grpn = load_group((s0 + G) / G);  // the next group, a group ahead
             if constexpr (DV_WORDS) {
                 if ((s & 3) == 0 && s + 4 < STEPS) dvn = dvp[(s >> 2) + 1];  // the next group's word, a group ahead
             }
@@ -497,7 +500,10 @@ void fused_gemm_kernel(FusedArgs a) {
             if constexpr (IQ1) {
                 fused_iq1(group_step(grp, j), sc.codes, ptab, d, p, words);
             } else {
-                fused_pools<MEMBER, K>(sc, lrow, s, kg, d, dvw, ptab, p);
+                // the lane's sub-blocks are those the one-step order gives
+                // step G(s/G) + kg's lane group j
+                fused_pools<MEMBER, K>(sc, lrow, G * (s / G) + (G > 1 ? kg : 0), G > 1 ? j : kg, d, dvw, ptab, p);
+                const uint4_t q = group_step(grp, j);
 #pragma unroll
                 for (int w = 0; w < 4; ++w) words[w] = q[w];
             }
@@ -530,13 +536,8 @@ void fused_gemm_kernel(FusedArgs a) {
                     }
                 }
             }
-            if (more) {
-                store_x((s + 1) & 1, xa, slot_blocks);  // the buffer every wavefront finished reading before the last barrier
-                if constexpr (!IQ1) q = qn;
-            }
-            if constexpr (IQ1) {
-                if (j == G - 1) grp = grpn;
-            }
+            if (more) store_x((s + 1) & 1, xa, slot_blocks);  // the buffer every wavefront finished reading before the last barrier
+            if (j == G - 1) grp = grpn;
             if constexpr (DV_WORDS) {
                 if ((s & 3) == 3) dvw = dvn;
             }
