@@ -273,8 +273,8 @@ void fused_gemm_kernel(FusedArgs a) {
     // Steps a code-word group: IQ1_S_R4 4, the IQ2 members 1.  Two-step
     // groups for the IQ2 members measured within 1% (IQ2_K gate 404.4 ->
     // 402.6 us, IQ2_KS gate 381.9 -> 380.8 us with 32 bytes of spills at 128
-    // VGPRs; IQ2_K at 2048 wide has no room for them): their lines are
-    // loaded four times a step-group of one already.
+    // VGPRs; IQ2_K at 2048 wide has no room for them): with one step a
+    // group, a line of their code plane is loaded four times, not 8 or 16.
     constexpr int G = IQ1 ? 4 : 1;
     static_assert(STEPS % G == 0, "whole groups of steps");
     __shared__ TileScan ts;
@@ -356,6 +356,8 @@ void fused_gemm_kernel(FusedArgs a) {
         const bool xv = xrow < a.n_x_rows;
         // a dead slot reads row 0 (the entry point refuses an empty x); its
         // products feed only its own output row, never stored as a value
+        // chunks 8 .. 15 (lane group 1's half of a step) start 64G elements
+        // after chunks 0 .. 7 in x, 64 in the staged row (see x_step)
         xoff[i] = (xv ? xrow : 0u) * uint32_t(2 * K) + uint32_t(16 * xchunk) + (xchunk >= 8 ? 128u * (G - 1) : 0u);
         xlive[i] = !IQ1 || xp < gend;
         if (xchunk == 0) {  // one thread a slot: the epilogue's destination, read once
