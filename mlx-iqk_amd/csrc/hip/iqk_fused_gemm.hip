@@ -6,9 +6,12 @@
 // sorted pairs (nn.py:221-238).  Here each workgroup decodes the weight rows
 // it needs straight into MFMA operands, so a prefill reads the 2-bit streams
 // (1122 B per 4096-wide IQ2_KS row) instead of writing and re-reading 8 KiB of
-// fp16 per row.  The weights are the producer's fp16 values bit for bit (the
-// same four-entry tables); only the f32 summation order differs from the
-// producer + grouped GEMM route.
+// fp16 per row.  IQ2_K's operands are the producer's fp16 weights bit for bit
+// (the same four-entry tables).  IQ2_KS and IQ1_S_R4 scale each weight row by
+// one fp16 d, so their operands are the exact products n = idx v (IQ1_S_R4:
+// (2s+1)(g + shift)), fp16 without rounding, and d multiplies the row's f32
+// sums once in the epilogue: a weight enters as d n instead of fp16(d n), and
+// a one-hot activation row still yields fp16(d n), the producer's weight.
 //
 // Work list: as the grouped GEMM, with group g = expert g: the slots (pair
 // rows) are sorted by expert, expert g owns [offs[g], offs[g+1]), and a block
@@ -134,8 +137,8 @@ __device__ __forceinline__ void copy_plane(const uint8_t *src, int rows, uint8_t
 
 // IQ2_K's exact pool products n_c = v_c x m (m = nibble - 8 the scale index,
 // v the alphabet), as fp16 pairs (word 0: n0 | n1 << 16, word 1: n2 | n3 <<
-// 16), by (alphabet << 4 | nibble).  Each is the fp16 product make_pool_h
-// forms, signed zeros included (a negative value times a zero index is -0).
+// 16), by (alphabet << 4 | nibble), each exact in fp16 (|n| <= 248), signed
+// zeros included (a negative value times a zero index is -0).
 struct Iq2kProducts {
     uint32_t w[2 * 32];
 };
@@ -177,11 +180,59 @@ constexpr Iq1Products make_iq1_products() {
     return t;
 }
 
-__constant__ const Iq1Products kIq1Products = make_iq1_products();
+// A four-entry fp16 table (n0 | n1 << 16, n2 | n3 << 16) as a v_perm pool:
+// the low bytes of n0 .. n3, then their high bytes.
+constexpr uint2_t split_pool(uint32_t n01, uint32_t n23) {
+    return {(n01 & 0xffu) | ((n01 >> 8) & 0xff00u) | ((n23 & 0xffu) << 16) | ((n23 & 0xff0000u) << 8),
+            ((n01 >> 8) & 0xffu) | ((n01 >> 16) & 0xff00u) | (((n23 >> 8) & 0xffu) << 16) | ((n23 >> 24) << 24)};
+}
 
-// The pool d x n_c from the products at byte `off` of the LDS table.  The
-// words pass as scalars: __builtin_bit_cast of a vector element (n.y of a
-// uint2_t) reads the vector's first element in this compiler.
+// IQ1_S_R4's products as pools.
+struct Iq1Pools {
+    uint2_t p[16];
+};
+
+constexpr Iq1Pools make_iq1_pools() {
+    Iq1Pools t{};
+    const Iq1Products q = make_iq1_products();
+    for (int e = 0; e < 16; ++e) t.p[e] = split_pool(q.w[2 * e], q.w[2 * e + 1]);
+    return t;
+}
+
+__constant__ const Iq1Pools kIq1Pools = make_iq1_pools();
+
+// IQ2_KS's exact products n_c = v_c x idx as pools, by (alphabet << 5 |
+// idx + 16): |n| <= 496, so each is exact in fp16 (a negative value times a
+// zero index is -0, as in the producer's chain).
+struct Iq2ksPools {
+    uint2_t p[64];
+};
+
+constexpr Iq2ksPools make_iq2ks_pools() {
+    Iq2ksPools t{};
+    constexpr int v[2][4] = {{-31, -13, 1, 17}, {-26, -8, 6, 22}};
+    for (int alpha = 0; alpha < 2; ++alpha)
+        for (int i5 = 0; i5 < 32; ++i5) {
+            const _Float16 m = _Float16(short(i5 - 16));
+            uint32_t w[2] = {0u, 0u};
+            for (int c = 0; c < 4; ++c) {
+                const _Float16 n = _Float16(short(v[alpha][c])) * m;
+                w[c / 2] |= uint32_t(__builtin_bit_cast(uint16_t, n)) << (16 * (c % 2));
+            }
+            t.p[32 * alpha + i5] = split_pool(w[0], w[1]);
+        }
+    return t;
+}
+
+__constant__ const Iq2ksPools kIq2ksPools = make_iq2ks_pools();
+
+// The pool d x n_c from exact fp16 products n_c: one correctly rounded
+// packed fp16 multiply a pair.  The producer's f32 chain forms the same exact
+// product (at most 11 + 9 significant bits, so no f32 rounding) and rounds
+// it to fp16 once, so the entries are equal bit for bit, signed zeros
+// included.  The words pass as scalars: __builtin_bit_cast of a vector
+// element (n.y of a uint2_t) reads the vector's first element in this
+// compiler.
 __device__ __forceinline__ Pool scale_products(uint32_t n01, uint32_t n23, _Float16 d) {
     const uint32_t p01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, n01) * d);
     const uint32_t p23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, n23) * d);
@@ -190,16 +241,18 @@ __device__ __forceinline__ Pool scale_products(uint32_t n01, uint32_t n23, _Floa
 
 // The v_perm tables of lane (row, kg) at step s, one per 16-weight word of
 // its 64 weights: IQ2_KS sub-blocks 4s + 2kg + h (two words each), IQ2_K
-// sub-blocks 8s + 4kg + w (one word each).  The same fp16 products as the
-// producer's f32 chain (make_pool_h); IQ2_K reads its products n = v x m
-// from the LDS table `ptab` (measured 4% faster on its fused projections than
-// forming them; IQ2_KS, two tables a step, measured the same either way).
-// IQ2_K's super-block scale comes from the dv plane, or (no dv plane in
-// LDS) from dvw, the lane's dv word of steps 4(s/4) .. +3 (scales of
-// super-blocks 2(s/4) and 2(s/4)+1).
+// sub-blocks 8s + 4kg + w (one word each).  IQ2_KS's tables are its exact
+// products idx v (the row scale d is applied to the sums), one LDS read of
+// `ptab` by (alphabet, scale index): against forming d idx v in fp16 a step
+// (two tables), the Zipf prefill's gate projection measured 381.1 -> 365.1
+// us.  IQ2_K's are d n with n = v x m from `ptab`, its d being per
+// super-block: the same fp16 products as the producer's f32 chain.  IQ2_K's
+// super-block scale comes from the dv plane, or (no dv plane in LDS) from
+// dvw, the lane's dv word of steps 4(s/4) .. +3 (scales of super-blocks
+// 2(s/4) and 2(s/4)+1).
 template <int MEMBER, int K>
-__device__ __forceinline__ void fused_pools(const FusedScales<MEMBER, K> &sc, int row, int s, int kg, _Float16 d,
-                                            uint32_t dvw, const uint2_t *ptab, Pool *p) {
+__device__ __forceinline__ void fused_pools(const FusedScales<MEMBER, K> &sc, int row, int s, int kg, uint32_t dvw,
+                                            const uint2_t *ptab, Pool *p) {
     using S = FusedScales<MEMBER, K>;
     if constexpr (MEMBER == IQ2_KS) {
         const uint32_t scl = sc.scl[row * S::SCL_S + 2 * s + kg];  // nibbles of sub-blocks 4s+2kg, +1
@@ -208,9 +261,10 @@ __device__ __forceinline__ void fused_pools(const FusedScales<MEMBER, K> &sc, in
         const int bit = 4 * (s & 1) + 2 * kg;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const int idx = int(((scl >> (4 * h)) & 15u) | (((hb >> (bit + h)) & 1u) << 4)) - 16;
-            const bool alpha = (ab >> (bit + h)) & 1u;
-            p[2 * h] = make_pool_h(d, _Float16(short(idx)), iq2_pair(alpha, 0), iq2_pair(alpha, 1));
+            // alphabet << 5 | the 5-bit scale index (idx + 16)
+            const uint32_t e = ((scl >> (4 * h)) & 15u) | (((hb >> (bit + h)) & 1u) << 4) | (((ab >> (bit + h)) & 1u) << 5);
+            const uint2_t q = ptab[e];
+            p[2 * h] = {q.x, q.y};
             p[2 * h + 1] = p[2 * h];
         }
     } else {
@@ -240,17 +294,19 @@ __device__ __forceinline__ void fused_pools(const FusedScales<MEMBER, K> &sc, in
 }
 
 // IQ1_S_R4 at one step: blocks b = 0, 1 of the lane (index bytes q[b], qh
-// word b of q.z).  Pools p[2b], p[2b+1] are block b's (d times the products
-// (2s+1) (g + shift) from the LDS table `ptab`: the producer's values), and
-// word 2b+t holds the grid codes of the block's 8-weight groups 2t and 2t+1.
-__device__ __forceinline__ void fused_iq1(uint4_t q, const uint16_t *grid, const uint2_t *ptab, _Float16 d, Pool *p,
+// word b of q.z).  Pools p[2b], p[2b+1] are block b's (the products
+// (2s+1) (g + shift) from the LDS table `ptab`; the row scale d is applied
+// to the sums: 394.9 -> 377.4 us on the Zipf prefill's gate projection
+// against forming d (2s+1) (g + shift) a block), and word 2b+t holds the grid
+// codes of the block's 8-weight groups 2t and 2t+1.
+__device__ __forceinline__ void fused_iq1(uint4_t q, const uint16_t *grid, const uint2_t *ptab, Pool *p,
                                           uint32_t *words) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
         const uint32_t qw = q[b], h = (q.z >> (16 * b)) & 0xffffu;
         // grid field 3 never occurs: four products, by qh bits 12-15
         const uint2_t n = ptab[(h >> 12) & 15u];
-        p[2 * b] = scale_products(uint32_t(n.x), uint32_t(n.y), d);
+        p[2 * b] = {n.x, n.y};
         p[2 * b + 1] = p[2 * b];
         uint32_t c[4];
 #pragma unroll
@@ -282,7 +338,7 @@ void fused_gemm_kernel(FusedArgs a) {
     // per slot of the tile: its output row, bit 31 set when its activations
     // are real (else its output row is NaN), or kNoStore
     __shared__ uint32_t slot_dst[kFusedBM];
-    __shared__ uint2_t ptab[MEMBER == IQ2_K ? 32 : IQ1 ? 16 : 1];  // IQ2_K's and IQ1_S_R4's pool products
+    __shared__ uint2_t ptab[MEMBER == IQ2_K ? 32 : IQ1 ? 16 : 64];  // pool products (IQ2_K) or pools
     constexpr uint32_t kNoStore = 0x7fffffffu;  // above any row (n_slots <= 2^30)
     __shared__ __attribute__((aligned(16))) std::conditional_t<IQ1, FusedGrid, S> sc;
 
@@ -313,7 +369,9 @@ void fused_gemm_kernel(FusedArgs a) {
     if constexpr (MEMBER == IQ2_K) {
         if (tid < 32) ptab[tid] = reinterpret_cast<const uint2_t *>(kIq2kProducts.w)[tid];
     } else if constexpr (IQ1) {
-        if (tid < 16) ptab[tid] = reinterpret_cast<const uint2_t *>(kIq1Products.w)[tid];
+        if (tid < 16) ptab[tid] = kIq1Pools.p[tid];
+    } else {
+        if (tid < 64) ptab[tid] = kIq2ksPools.p[tid];
     }
     // scale planes of the block's rows (IQ1_S_R4: the grid codes)
     if constexpr (IQ1) {
@@ -467,9 +525,9 @@ void fused_gemm_kernel(FusedArgs a) {
     CodeGroup grp = load_group(0), grpn{};
     store_x(0, xa, kAllPasses);
     __syncthreads();  // scale planes and the first activations are in LDS
-    // row scale: IQ2_KS from LDS (rows past out_features read LDS junk, never
-    // stored), IQ1_S_R4 from its stream (an in-bounds row); IQ2_K's are per
-    // super-block
+    // row scale, applied to the sums: IQ2_KS from LDS (rows past out_features
+    // read LDS junk, never stored), IQ1_S_R4 from its stream (an in-bounds
+    // row); IQ2_K's are per super-block, in its pools
     _Float16 d = 0.f16;
     if constexpr (MEMBER == IQ2_KS)
         d = half_of_bits(*reinterpret_cast<const uint16_t *>(sc.dv + lrow * S::DV_S));
@@ -500,11 +558,11 @@ void fused_gemm_kernel(FusedArgs a) {
             Pool p[4];
             uint32_t words[4];
             if constexpr (IQ1) {
-                fused_iq1(group_step(grp, j), sc.codes, ptab, d, p, words);
+                fused_iq1(group_step(grp, j), sc.codes, ptab, p, words);
             } else {
                 // the lane's sub-blocks are those the one-step order gives
                 // step G(s/G) + kg's lane group j
-                fused_pools<MEMBER, K>(sc, lrow, G * (s / G) + (G > 1 ? kg : 0), G > 1 ? j : kg, d, dvw, ptab, p);
+                fused_pools<MEMBER, K>(sc, lrow, G * (s / G) + (G > 1 ? kg : 0), G > 1 ? j : kg, dvw, ptab, p);
                 const uint4_t q = group_step(grp, j);
 #pragma unroll
                 for (int w = 0; w < 4; ++w) words[w] = q[w];
@@ -547,6 +605,7 @@ void fused_gemm_kernel(FusedArgs a) {
           }
         }
 
+        const float dscale = float(d);
         // D layout (32x32): lane l, register r holds row 8(r/4) + 4(l/32) +
         // r%4 of column l % 32.
         if (!wv) return;
@@ -557,7 +616,8 @@ void fused_gemm_kernel(FusedArgs a) {
                 const uint32_t dst = slot_dst[32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3)];
                 if (dst != kNoStore)
                     a.y[size_t(dst & 0x7fffffffu) * a.N + n0 + lrow] =
-                        (dst >> 31) ? uint16_t(float_to_half_bits(acc[mb][r])) : kHalfNaN;
+                        (dst >> 31) ? uint16_t(float_to_half_bits(MEMBER == IQ2_K ? acc[mb][r] : acc[mb][r] * dscale))
+                                    : kHalfNaN;
             }
         }
     };

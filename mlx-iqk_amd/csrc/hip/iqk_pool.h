@@ -3,9 +3,8 @@
 //
 // Bit-exactness: a sub-block's four weights are the CPU dequantizer's f32
 // chain dl = d * float(index), y = dl * float(value) (each product exact),
-// rounded once to fp16 (make_pool), or the same exact product formed in fp16
-// and rounded once (make_pool_h).  They are formed once per sub-block, and each pair of
-// output weights is one v_perm_b32 from that 8-byte table.
+// rounded once to fp16 (make_pool).  They are formed once per sub-block, and
+// each pair of output weights is one v_perm_b32 from that 8-byte table.
 #ifndef IQK_POOL_H
 #define IQK_POOL_H
 
@@ -33,31 +32,6 @@ __device__ __forceinline__ Pool make_pool(float dl, float v0, float v1, float v2
     const uint32_t p01 = float_to_half_bits(y0) | (float_to_half_bits(y1) << 16);
     const uint32_t p23 = float_to_half_bits(y2) | (float_to_half_bits(y3) << 16);
     return {perm(p23, p01, 0x06040200u), perm(p23, p01, 0x07050301u)};
-}
-
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-
-// The same four entries d * m * v_c from an fp16 scale d, a multiplier m and
-// values v_c whose products m v_c are exact in fp16 (IQ2 members: m the scale
-// index, |m v_c| <= 496), in two packed fp16 multiplies a pair: n = v m
-// (exact), then n d, one correctly rounded fp16 multiply.  The f32 chain above
-// forms the same exact product (at most 11 + 9 significant bits, so no f32
-// rounding) and rounds it to fp16 once, so the entries are equal bit for bit,
-// signed zeros included (the sign of m v_c d is the same however the product
-// is grouped).  Fewer instructions than the f32 chain: the fused GEMM's IQ2
-// pools use it (its VALU bounds it); the producer, bound by its stores, and
-// the IQ1_S_R4 pools measured slower with it and keep the f32 chain.
-__device__ __forceinline__ Pool make_pool_h(_Float16 d, _Float16 m, half2_t v01, half2_t v23) {
-    const half2_t n01 = v01 * m, n23 = v23 * m;
-    const uint32_t p01 = __builtin_bit_cast(uint32_t, n01 * d), p23 = __builtin_bit_cast(uint32_t, n23 * d);
-    return {perm(p23, p01, 0x06040200u), perm(p23, p01, 0x07050301u)};
-}
-
-// The IQ2 alphabets as fp16 pairs: (-31, -13), (1, 17) and the shifted
-// (-26, -8), (6, 22).
-__device__ __forceinline__ half2_t iq2_pair(bool alpha, int hi) {
-    return hi ? (alpha ? half2_t{6.f16, 22.f16} : half2_t{1.f16, 17.f16})
-              : (alpha ? half2_t{-26.f16, -8.f16} : half2_t{-31.f16, -13.f16});
 }
 
 __device__ __forceinline__ _Float16 half_of_bits(uint32_t bits) { return __builtin_bit_cast(_Float16, uint16_t(bits)); }

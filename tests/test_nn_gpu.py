@@ -600,7 +600,7 @@ def test_sorted_matmul_range_matches_a_float64_reference(device, member, fused):
         module.fused_prefill = True
 
 
-# -- fused prefill (the producer's weights formed inside the GEMM) ----------
+# -- fused prefill (the weights formed inside the GEMM) ---------------------
 
 
 def _both_routes(module, *args, **kw):
@@ -615,7 +615,9 @@ def _both_routes(module, *args, **kw):
 @pytest.mark.parametrize("member", fmt.MEMBERS)
 @pytest.mark.parametrize("n", (2048, 4096))
 def test_fused_prefill_matches_the_producer_route(device, member, n):
-    """Same fp16 weights, f32 sums in another order: the two routes agree to
+    """The producer route sums fp16 weights; the fused GEMM sums IQ2_K's same
+    fp16 weights, and IQ2_KS's and IQ1_S_R4's exact products n scaled by
+    the row scale d afterwards, in another order: the two routes agree to
     fp16 rounding, and each meets the float64 gate."""
     print(f"fused prefill {member} n={n}", flush=True)
     module, ref = _module(member, n, wirepack.seed_for(member, n, "fused"), device)
@@ -704,12 +706,14 @@ def test_fused_prefill_experts_of_many_tiles(device, member, n):
 @pytest.mark.parametrize("scales", ("serving", "tiny"))
 def test_fused_prefill_weights_are_the_producers(device, member, n, scales):
     """A one-hot activation row e_k makes a fused output the weight column k
-    itself: one product w * 1 and zeros, exact in f32 and again in fp16.  So
+    itself: one product w * 1 and zeros, exact in f32 and again in fp16 (IQ2_K,
+    whose operands are the fp16 weights), or the exact product n * 1 times the
+    row scale d, exact in f32 and rounded once to fp16 (IQ2_KS, IQ1_S_R4).  So
     every decoded weight the fused GEMM forms in registers is checked against
     the producer's dequantized stack by value (a -0 weight comes out +0 after
     the zero products, so zeros compare by value).  `tiny` scales are all
-    subnormal, so many table entries are subnormal or round to zero: the fp16
-    table arithmetic must round them as the producer's f32 chain does."""
+    subnormal, so many weights are subnormal or round to zero: the fused
+    arithmetic must round them as the producer's f32 chain does."""
     print(f"fused weights {member} n={n} {scales}", flush=True)
     wire = wirepack.random_wire(member, EXPERTS * OUT, n, seed=wirepack.seed_for(member, n, "onehot"), scales=scales)
     shapes = fmt.component_shapes(member, EXPERTS, OUT, n)
