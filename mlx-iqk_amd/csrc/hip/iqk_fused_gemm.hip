@@ -43,8 +43,8 @@
 // IQ1_S_R4: the lane's two 32-weight blocks of a step bring their index bytes
 // and qh words with the step's loads (no scale planes), and the block's 4 KiB
 // of grid codes sit in LDS; two grid entries make one 16-code word, expanded
-// with the producer's pool of the block, so the weights are again the
-// producer's.
+// with the block's pool of exact products (2s+1)(g + shift), the row's d
+// applied to the sums as for IQ2_KS.
 
 #include <type_traits>
 
@@ -308,11 +308,14 @@ __device__ __forceinline__ void fused_iq1(uint4_t q, const uint16_t *grid, const
         const uint2_t n = ptab[(h >> 12) & 15u];
         p[2 * b] = {n.x, n.y};
         p[2 * b + 1] = p[2 * b];
-        uint32_t c[4];
+        // two 16-bit codes a word, joined as a vector (one v_perm; as
+        // c0 | c1 << 16 the compiler spent two ops: 384.8 -> 380.2 us)
+        typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
+        uint16_t c[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) c[t] = grid[((qw >> (8 * t)) & 0xffu) | (((h >> (3 * t)) & 7u) << 8)];
-        words[2 * b] = c[0] | (c[1] << 16);
-        words[2 * b + 1] = c[2] | (c[3] << 16);
+        words[2 * b] = __builtin_bit_cast(uint32_t, u16x2_t{c[0], c[1]});
+        words[2 * b + 1] = __builtin_bit_cast(uint32_t, u16x2_t{c[2], c[3]});
     }
 }
 
