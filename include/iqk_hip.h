@@ -180,16 +180,19 @@ int iqk_grouped_gemm(int64_t in_features, int64_t out_features, int64_t n_groups
                      const void *x, int64_t n_x_rows, const void *w, const uint32_t *group_offsets,
                      const uint32_t *x_rows, const uint32_t *y_rows, void *y, void *stream);
 
-// Fused prefill contraction straight from the streams: the producer's fp16
-// weights formed inside an fp16 MFMA grouped GEMM, never stored (replaces
-// dequant_kernel / dequant_range_kernel + mx.gather_mm(x, W.swapaxes(-1,-2),
-// rhs_indices, sorted_indices=True), src/mlx_iqk/nn.py:155-238).  Slots are
-// sorted by expert; expert e owns slots [group_offsets[e], group_offsets[e+1]):
+// Fused prefill contraction straight from the streams: the weights formed
+// inside an fp16 MFMA grouped GEMM, never stored (replaces dequant_kernel /
+// dequant_range_kernel + mx.gather_mm(x, W.swapaxes(-1,-2), rhs_indices,
+// sorted_indices=True), src/mlx_iqk/nn.py:155-238).  Slots are sorted by
+// expert; expert e owns slots [group_offsets[e], group_offsets[e+1]):
 //   y[y_rows[p]][n] = fp16( sum_k x[x_rows[p]][k] * W[e][row_start + n][k] ),
-// 0 <= n < rows, with W iqk_dequant's fp16 value bit for bit and f32
-// accumulation (the summation order differs from iqk_dequant +
-// iqk_grouped_gemm; it does not depend on row_start, so row ranges
-// concatenate to the full call bit for bit).  y: f16 [n_slots, rows];
+// 0 <= n < rows, f32 accumulation.  IQ2_K: W is iqk_dequant's fp16 value bit
+// for bit.  IQ2_KS, IQ1_S_R4 (one scale d a row): the sum runs over the
+// exact products n = W / d and is multiplied by d once, so W enters
+// unrounded (a one-hot x row yields iqk_dequant's fp16 weight).  The
+// summation order differs from iqk_dequant + iqk_grouped_gemm; it does not
+// depend on row_start, so row ranges concatenate to the full call bit for
+// bit.  y: f16 [n_slots, rows];
 // group_offsets: u32 [num_experts + 1] (device, non-decreasing, last =
 // n_slots); x, x_rows, y_rows as iqk_grouped_gemm.  IQK_ERR_GEOMETRY unless
 // 0 <= row_start < row_start + rows <= out_features.  All three members.

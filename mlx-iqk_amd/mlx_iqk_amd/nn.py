@@ -80,9 +80,11 @@ class IqkSwitchLinear(torch.nn.Module):
 
     mode = "iqk"
     fused_prefill = True
-    """Prefill through the fused contraction (the producer's fp16 weights
-    formed inside the GEMM, never stored) rather than producer + grouped GEMM.
-    Both give the same weights; the f32 summation order differs."""
+    """Prefill through the fused contraction (the weights formed inside the
+    GEMM, never stored) rather than producer + grouped GEMM.  IQ2_K's are the
+    producer's fp16 weights; IQ2_KS and IQ1_S_R4 sum the exact products and
+    apply the row scale to the sums, so their weights enter unrounded.  The
+    f32 summation order differs too; both routes meet the same float64 gate."""
 
     def __init__(self, member: str, num_experts: int, out_features: int, in_features: int,
                  device=None):
