@@ -200,6 +200,8 @@ def _gemv_launch(kind: int, member: str, n: int, out_features: int, num_experts:
     operands already checked: device addresses of x, sel and y, the streams'
     pointer array.  gridDim.y carries the pair index, so the pairs go in
     chunks that keep whole activation rows together."""
+    if not 0 < pairs_per_row <= 65535:  # one launch takes at most 65535 pairs
+        raise IqkKernelError(f"{pairs_per_row} pairs a row: a decode launch takes 1 .. 65535 pairs of one row")
     fast = _native.launcher()
     lib = None if fast is not None else _native.load()
     ptrs_addr = ctypes.addressof(ptrs)

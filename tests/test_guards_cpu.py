@@ -5,6 +5,7 @@ src/mlx_iqk/kernels.py:100-142 and src/mlx_iqk/nn.py)."""
 
 from __future__ import annotations
 
+import ctypes
 import pathlib
 import re
 
@@ -99,3 +100,13 @@ def test_the_abi_stream_order_is_the_format_order():
         want = fmt.component_dtypes(member)
         assert names == list(want) and int(count) == len(want)
         assert types == [want[k].name for k in names]
+
+
+def test_a_row_of_more_pairs_than_one_launch_takes_is_refused():
+    """A launch carries at most 65535 pairs; one activation row with more
+    pairs than that cannot be split between launches, so it is refused before
+    anything launches (the pointers below are never dereferenced)."""
+    ptrs = (ctypes.c_void_p * 5)(*([16] * 5))
+    for ppr in (65536, 70000, 0):
+        with pytest.raises(IqkKernelError):
+            kernels._gemv_launch(0, "iq2_ks", 4096, 32, 8, 16, ptrs, 5, 16, ppr, ppr, 16, 0)
