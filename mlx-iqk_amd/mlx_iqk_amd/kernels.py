@@ -228,11 +228,19 @@ def gemv_checked(member: str, x: torch.Tensor, streams: "CheckedStreams", sel: t
     elements, all on the streams' GPU, ``streams.gemv_ok`` and
     ``mats % rows == 0``.  (The switch module's eager decode path: it skips
     the reshapes and repeated checks of :func:`gemv`.)"""
-    if mats:
-        _gemv_launch(0, member, streams.key[3], out_features, num_experts, x.data_ptr(), streams.ptrs,
-                     streams.count, sel.data_ptr(), mats // rows, mats, out.data_ptr(),
-                     _raw_stream(streams.device_index) if _raw_stream is not None
-                     else torch.cuda.current_stream(streams.device).cuda_stream)
+    if not mats:
+        return
+    stream = (_raw_stream(streams.device_index) if _raw_stream is not None
+              else torch.cuda.current_stream(streams.device).cuda_stream)
+    fast = _native.launcher()
+    if fast is not None and mats <= 65535:  # one launch: the binding's call with nothing else around it
+        rc = fast.gemv(0, _native.MEMBER_IDS[member], streams.key[3], out_features, num_experts, x.data_ptr(),
+                       streams.ptrs_addr, streams.count, sel.data_ptr(), mats // rows, mats, out.data_ptr(), stream)
+        if rc:
+            _native.check(rc, f"iqk_gemv({member}, {streams.key[3]}x{out_features})")
+        return
+    _gemv_launch(0, member, streams.key[3], out_features, num_experts, x.data_ptr(), streams.ptrs, streams.count,
+                 sel.data_ptr(), mats // rows, mats, out.data_ptr(), stream)
 
 
 def stream_floor_words(nbytes: int, loads: int = 4, max_waves: int = 0) -> int:
