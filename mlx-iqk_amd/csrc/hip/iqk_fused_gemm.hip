@@ -41,10 +41,10 @@
 // the 32 rows a wavefront reads at once fall in distinct banks.
 //
 // IQ1_S_R4: the lane's two 32-weight blocks of a step bring their index bytes
-// and qh words with the step's loads (no scale planes), and the block's 4 KiB
-// of grid codes sit in LDS; two grid entries make one 16-code word, expanded
-// with the block's pool of exact products (2s+1)(g + shift), the row's d
-// applied to the sums as for IQ2_KS.
+// and qh words with the step's loads (no scale planes), and the grid sits in
+// LDS as each entry's pool selectors (16 KiB); two grid entries expand like
+// one 16-code word, with the block's pool of exact products (2s+1)(g +
+// shift), the row's d applied to the sums as for IQ2_KS.
 
 #include <type_traits>
 
@@ -297,10 +297,15 @@ __device__ __forceinline__ void fused_pools(const FusedScales<MEMBER, K> &sc, in
 // word b of q.z).  Pools p[2b], p[2b+1] are block b's (the products
 // (2s+1) (g + shift) from the LDS table `ptab`; the row scale d is applied
 // to the sums: 394.9 -> 377.4 us on the Zipf prefill's gate projection
-// against forming d (2s+1) (g + shift) a block), and word 2b+t holds the grid
-// codes of the block's 8-weight groups 2t and 2t+1.
-__device__ __forceinline__ void fused_iq1(uint4_t q, const uint16_t *grid, const uint2_t *ptab, Pool *p,
-                                          uint32_t *words) {
+// against forming d (2s+1) (g + shift) a block), and sels[2b+t] holds the
+// pool selectors of the block's 8-weight groups 2t and 2t+1, read whole from
+// the block's LDS table of them (grid_selectors): no shifts and masks a step.
+// Against 16-bit code words expanded by expand_word_paired (their selectors
+// formed a step) the Zipf prefill's gate projection measured 390.4 -> 379.1
+// us, bit-identical: 28 fewer VALU a step for four times the LDS bytes of
+// the lookups.
+__device__ __forceinline__ void fused_iq1(uint4_t q, const uint2_t *grid, const uint2_t *ptab, Pool *p,
+                                          uint4_t *sels) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
         const uint32_t qw = q[b], h = (q.z >> (16 * b)) & 0xffffu;
@@ -308,20 +313,38 @@ __device__ __forceinline__ void fused_iq1(uint4_t q, const uint16_t *grid, const
         const uint2_t n = ptab[(h >> 12) & 15u];
         p[2 * b] = {n.x, n.y};
         p[2 * b + 1] = p[2 * b];
-        // two 16-bit codes a word, joined as a vector (one v_perm; as
-        // c0 | c1 << 16 the compiler spent two ops: 384.8 -> 380.2 us)
-        typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
-        uint16_t c[4];
+        uint2_t c[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) c[t] = grid[((qw >> (8 * t)) & 0xffu) | (((h >> (3 * t)) & 7u) << 8)];
-        words[2 * b] = __builtin_bit_cast(uint32_t, u16x2_t{c[0], c[1]});
-        words[2 * b + 1] = __builtin_bit_cast(uint32_t, u16x2_t{c[2], c[3]});
+        sels[2 * b] = uint4_t{c[0].x, c[0].y, c[1].x, c[1].y};
+        sels[2 * b + 1] = uint4_t{c[2].x, c[2].y, c[3].x, c[3].y};
     }
 }
 
 struct FusedGrid {
-    uint16_t codes[IQK_IQ1S_GRID_SIZE];
+    uint2_t sel[IQK_IQ1S_GRID_SIZE];  // grid_selectors of every grid entry, 16 KiB
 };
+
+// Pool selectors of one grid entry (positions i at bits 2i): (p0, p4, p1,
+// p5) and (p2, p6, p3, p7), one position a byte.
+__device__ __forceinline__ uint2_t grid_selectors(uint32_t x) {
+    return {(x & 0x0303u) | ((x << 14) & 0x03030000u), ((x >> 4) & 0x0303u) | ((x << 10) & 0x03030000u)};
+}
+
+// The 16 weights of two grid entries from their selectors (sel.xy entry 0,
+// sel.zw entry 1), in expand_word_paired's output order for the 16-code word
+// of the two entries (dword 2j: positions j, j+4 of entry 0; dword 2j+1: of
+// entry 1), so the MFMAs and the staged activations are the same as for a
+// code word.
+__device__ __forceinline__ void expand_sel_paired(uint4_t sel, Pool p, uint32_t *out) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t e = sel[i];
+        const uint32_t lo = perm(p.lo, p.lo, e), hi = perm(p.hi, p.hi, e);
+        out[4 * (i & 1) + (i >> 1)] = perm(hi, lo, 0x05010400u);
+        out[4 * (i & 1) + (i >> 1) + 2] = perm(hi, lo, 0x07030602u);
+    }
+}
 
 template <int MEMBER, int K>
 __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(4)))
@@ -376,11 +399,13 @@ void fused_gemm_kernel(FusedArgs a) {
     } else {
         if (tid < 64) ptab[tid] = kIq2ksPools.p[tid];
     }
-    // scale planes of the block's rows (IQ1_S_R4: the grid codes)
+    // scale planes of the block's rows (IQ1_S_R4: the grid as pool selectors)
     if constexpr (IQ1) {
-        static_assert(IQK_IQ1S_GRID_SIZE * 2 / 16 <= kFusedThreads, "one 16-byte chunk of the grid per thread");
-        if (tid < IQK_IQ1S_GRID_SIZE * 2 / 16)
-            reinterpret_cast<uint4_t *>(sc.codes)[tid] = reinterpret_cast<const uint4_t *>(iqk_iq1s_grid_codes)[tid];
+        static_assert(IQK_IQ1S_GRID_SIZE == 4 * kFusedThreads, "four grid entries a thread");
+        const uint2_t cw = reinterpret_cast<const uint2_t *>(iqk_iq1s_grid_codes)[tid];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            sc.sel[4 * tid + i] = grid_selectors(((i < 2 ? cw.x : cw.y) >> (16 * (i & 1))) & 0xffffu);
     } else {
         copy_plane<S::SCL, S::SCL_S>(static_cast<const uint8_t *>(a.s1) + row0 * S::SCL, rows_here, sc.scl, tid);
     }
@@ -560,8 +585,9 @@ void fused_gemm_kernel(FusedArgs a) {
             }
             Pool p[4];
             uint32_t words[4];
+            uint4_t sels[IQ1 ? 4 : 1];
             if constexpr (IQ1) {
-                fused_iq1(group_step(grp, j), sc.codes, ptab, p, words);
+                fused_iq1(group_step(grp, j), sc.sel, ptab, p, sels);
             } else {
                 // the lane's sub-blocks are those the one-step order gives
                 // step G(s/G) + kg's lane group j
@@ -586,7 +612,10 @@ void fused_gemm_kernel(FusedArgs a) {
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
                 uint32_t bw[8];
-                expand_word_paired(words[w], p[w], bw);
+                if constexpr (IQ1)
+                    expand_sel_paired(sels[w], p[w], bw);
+                else
+                    expand_word_paired(words[w], p[w], bw);
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int u = 2 * w + h;
