@@ -9,6 +9,9 @@
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
 
+#include <limits.h>
+#include <stdint.h>
+
 #include "iqk_hip.h"
 
 #ifndef IQK_SOURCE_HASH
@@ -32,6 +35,13 @@ static PyObject *gemv(PyObject *self, PyObject *const *args, Py_ssize_t nargs) {
     long long v[13];
     for (int i = 0; i < 13; ++i)
         if (!as_i64(args[i], &v[i])) return NULL;
+    /* the narrow arguments: member and stream count (int), pairs per row and
+     * pair count (uint32); a value out of range is refused, not truncated */
+    if (v[1] < INT_MIN || v[1] > INT_MAX || v[7] < INT_MIN || v[7] > INT_MAX || v[9] < 0 || v[9] > UINT32_MAX ||
+        v[10] < 0 || v[10] > UINT32_MAX) {
+        PyErr_SetString(PyExc_OverflowError, "gemv: member, stream count, pairs per row or pair count out of range");
+        return NULL;
+    }
     int (*fn)(int, int64_t, int64_t, int64_t, const void *, const void *const *, int, const uint32_t *, uint32_t,
               uint32_t, void *, void *) = v[0] == 1 ? iqk_gemv_floor : v[0] == 2 ? iqk_gemv_floor_grid : iqk_gemv;
     const int rc = fn((int)v[1], (int64_t)v[2], (int64_t)v[3], (int64_t)v[4], (const void *)(uintptr_t)v[5],

@@ -197,3 +197,11 @@ def test_launch_binding_is_built_from_the_same_sources_and_refuses_as_the_abi(li
     assert fast.gemv(0, 0, 4096, 2048, 256, 16, addr, 5, 16, 6, 0, 16, 0) == 0  # no pairs: no launch
     with pytest.raises(TypeError):
         fast.gemv(0, 0, 4096)
+    # the narrow arguments are range-checked, not truncated into a valid call
+    for bad in ((0, 1 << 31, 4096, 2048, 256, 16, addr, 5, 16, 6, 12, 16, 0),   # member past int
+                (0, 0, 4096, 2048, 256, 16, addr, 1 << 32, 16, 6, 12, 16, 0),  # stream count past int
+                (0, 0, 4096, 2048, 256, 16, addr, 5, 16, (1 << 32) + 6, 12, 16, 0),  # pairs a row past u32
+                (0, 0, 4096, 2048, 256, 16, addr, 5, 16, 6, (1 << 32) + 12, 16, 0),  # pairs past u32
+                (0, 0, 4096, 2048, 256, 16, addr, 5, 16, 6, -12, 16, 0)):
+        with pytest.raises(OverflowError):
+            fast.gemv(*bad)
