@@ -521,7 +521,8 @@ def fused_matmul(member: str, x: torch.Tensor, streams: list[torch.Tensor], num_
                  row_start: int = 0, rows: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """Prefill contraction straight from the streams: ``y[y_rows[p]] = x[x_rows[p]] @ W[e, r0:r0+rows]^T``
     for the slots ``p`` of expert ``e`` (``[group_offsets[e], group_offsets[e+1])``), with
-    ``W`` the producer's fp16 weights formed inside the GEMM.  fp16 ``[P, rows]``."""
+    ``W`` formed inside the GEMM: IQ2_K's as the producer's fp16 weights, IQ2_KS's and
+    IQ1_S_R4's as exact products whose row scale multiplies the f32 sums.  fp16 ``[P, rows]``."""
     if member not in FUSED_MEMBERS:
         raise IqkKernelError(f"the fused prefill covers {FUSED_MEMBERS}; {member!r} takes the producer route")
     n = int(x.shape[-1])
